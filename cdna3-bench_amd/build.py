@@ -1,0 +1,69 @@
+"""Build the gfx950 library and the torch extension in-tree.
+
+1. ``make -C csrc`` -> ``mxfp4_cdna3/libmxfp4_mi355x.so`` (every HIP kernel
+   plus the extern "C" entry points of include/mxfp4_mi355x.h), hipcc
+   --offload-arch=gfx950.
+2. ``csrc/mxfp4_ext.cpp`` -> ``mxfp4_cdna3/_C<ext suffix>`` (pybind11 +
+   torch headers, linked against the library with an $ORIGIN rpath).
+
+Both steps run on a CPU-only host (hipcc cross-compiles).  Usage:
+``python cdna3-bench_amd/build.py [--jobs N]``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import subprocess
+import sys
+import sysconfig
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+PKG = os.path.join(HERE, "mxfp4_cdna3")
+REPO = os.path.dirname(HERE)
+INCLUDE = os.path.join(REPO, "include")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+
+def build_library(jobs: int = 8) -> str:
+    subprocess.run(["make", "-s", "-C", CSRC, f"-j{jobs}", f"OUT_DIR={PKG}"], check=True)
+    return os.path.join(PKG, "libmxfp4_mi355x.so")
+
+
+def build_extension() -> str:
+    import torch
+    from torch.utils import cpp_extension
+
+    suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    out = os.path.join(PKG, "_C" + suffix)
+    src = os.path.join(CSRC, "mxfp4_ext.cpp")
+    incs = cpp_extension.include_paths() + [sysconfig.get_paths()["include"], INCLUDE,
+                                            os.path.join(ROCM, "include")]
+    libdirs = cpp_extension.library_paths() + [PKG, os.path.join(ROCM, "lib")]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-w", src, "-o", out + ".tmp",
+           "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM", "-DTORCH_EXTENSION_NAME=_C",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={abi}"]
+    cmd += [f"-I{p}" for p in incs] + [f"-L{p}" for p in libdirs]
+    cmd += ["-lmxfp4_mi355x", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lc10_hip",
+            "-lamdhip64", "-Wl,-rpath,$ORIGIN"]
+    subprocess.run(cmd, check=True)
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build(jobs: int = 8) -> None:
+    build_library(jobs)
+    build_extension()
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--lib-only", action="store_true")
+    args = ap.parse_args()
+    build_library(args.jobs)
+    if not args.lib_only:
+        build_extension()
+    print("built", file=sys.stderr)

@@ -1,0 +1,376 @@
+// extern "C" entry points (include/mxfp4_mi355x.h): argument checks, the
+// 256-CU cost model that picks a kernel plan, workspace layout, launch.
+//
+// Reference counterparts: dispatch/check_inputs (csrc/mxfp4_ext.cpp:11-48),
+// launch_strategy_* (csrc/common.h:43-78), gemm_auto (python/mxfp4_cdna3/
+// kernels.py:63-74), shape_supported_* (csrc/common.h:80-99), device_info
+// (csrc/mxfp4_ext.cpp:156-168), cost_model.predict (python/mxfp4_cdna3/
+// cost_model.py:117-146).
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+
+#include "mxfp4_kernels.h"
+#include "../../include/mxfp4_mi355x.h"
+
+namespace mxfp4 {
+namespace {
+
+// ---- MI355X roofline constants (dense, no sparsity) ------------------------
+constexpr double kNumCus = 256.0;
+constexpr double kHbmBytesPerS = 8.0e12;
+constexpr double kMfmaFlopsPerS = 2.5e15;
+constexpr double kLaunchS = 2.0e-6;  // fixed per-launch cost folded into every plan
+
+struct TiledVariant {
+  TiledShape shape;
+  double eff;       // sustained fraction of the CU's MFMA peak
+  int ctas_per_cu;  // residency (registers / LDS)
+};
+
+// Tile variants of the tiled family; index = mxfp4_plan.variant.
+const TiledVariant kTiled[] = {
+    {{2, 2, 4}, 0.70, 1},  // 0: 256 x 256, 4 waves, 128 x 128 per wave
+    {{4, 2, 2}, 0.70, 1},  // 1: 256 x 256, 8 waves
+    {{2, 2, 2}, 0.60, 2},  // 2: 128 x 256
+    {{1, 2, 2}, 0.45, 2},  // 3:  64 x 256
+    {{2, 1, 2}, 0.50, 2},  // 4: 128 x 128
+    {{1, 2, 1}, 0.30, 4},  // 5:  32 x 256
+};
+constexpr int kNumTiled = sizeof(kTiled) / sizeof(kTiled[0]);
+
+// Shapes of the memory-bound family; index = mxfp4_plan.variant.
+const GemvShape kGemv[] = {
+    {1, 16, 4}, {1, 8, 8}, {1, 8, 4}, {1, 4, 8}, {2, 8, 4},
+    {2, 4, 8},  {1, 2, 8}, {2, 2, 8}, {1, 2, 16}, {2, 2, 16},
+};
+constexpr int kNumGemv = sizeof(kGemv) / sizeof(kGemv[0]);
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+double problem_bytes(int64_t M, int64_t N, int64_t K, int c_bytes) {
+  return 2.0 * M * K + N * K / 2.0 + N * K / 32.0 + (double)c_bytes * M * N;
+}
+
+int gemv_steps(int layout, int64_t K) { return (int)(layout == kLayoutKN ? K / 32 : ceil_div(K, 128)); }
+
+// Partial-tile floats per CTA of the memory-bound family.
+int64_t gemv_tile(const GemvShape& g) { return 16LL * g.mt * 16 * g.cb; }
+
+bool gemv_plan_ok(int layout, int64_t M, int64_t N, const GemvShape& g) {
+  if (M > 16 * g.mt) return false;
+  if (layout == kLayoutKN && (N % 16 != 0 || g.cb < 4)) return false;
+  return gemv_shape_available(layout, g);
+}
+
+// Memory-bound family: pick the shape and split count that keep enough bytes
+// in flight (>= 2 CTAs of 8+ waves per CU) with at least two K steps per wave.
+void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
+  const int mt = M <= 16 ? 1 : 2;
+  int want = -1;
+  for (int i = 0; i < kNumGemv; ++i) {
+    const GemvShape& g = kGemv[i];
+    if (g.mt != mt) continue;
+    if (layout == kLayoutKN && g.cb == 8 && g.wpc == (mt == 1 ? 8 : 4)) want = i;
+    if (layout == kLayoutNK && g.cb == 2 && g.wpc == 16) want = i;
+  }
+  const GemvShape& g = kGemv[want];
+  const int64_t cols = 16 * g.cb;
+  const int64_t groups = ceil_div(N, cols);
+  const int64_t steps = gemv_steps(layout, K);
+  const int64_t target = layout == kLayoutKN ? 512 : 256;
+  int64_t splits = std::max<int64_t>(1, ceil_div(target, groups));
+  splits = std::min<int64_t>(splits, std::max<int64_t>(1, steps / (2 * g.wpc)));
+  out->kernel = MXFP4_KERNEL_GEMV;
+  out->variant = want;
+  out->split_k = (int32_t)splits;
+  out->reserved = 0;
+}
+
+double tiled_time(const TiledVariant& v, int64_t M, int64_t N, int64_t K, int splits) {
+  const int bm = v.shape.bm(), bn = v.shape.bn();
+  const int64_t tiles = ceil_div(M, bm) * ceil_div(N, bn);
+  const int64_t ksteps = ceil_div(K, 64);
+  const int64_t per_split = ceil_div(ksteps, splits);
+  const int64_t ctas = tiles * ceil_div(ksteps, per_split);
+  const double slots = kNumCus * v.ctas_per_cu;
+  const double rounds = std::ceil((double)ctas / slots);
+  const double cu_rate = kMfmaFlopsPerS / kNumCus * v.eff;
+  const double t_cta = (double)bm * bn * per_split * 64 * 2.0 * v.ctas_per_cu / cu_rate;
+  double t = rounds * t_cta;
+  const double t_hbm = problem_bytes(M, N, K, 2) / kHbmBytesPerS;
+  t = std::max(t, t_hbm);
+  if (splits > 1) t += 2.0 * tiles * splits * (double)bm * bn * 4.0 / kHbmBytesPerS + t_cta / 8;
+  return t + kLaunchS;
+}
+
+void choose_tiled(int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
+  double best = 1e30;
+  int bv = 0, bs = 1;
+  const int64_t ksteps = ceil_div(K, 64);
+  for (int v = 0; v < kNumTiled; ++v) {
+    const TiledVariant& tv = kTiled[v];
+    const int64_t tiles = ceil_div(M, tv.shape.bm()) * ceil_div(N, tv.shape.bn());
+    for (int s = 1; s <= 16 && s <= ksteps; ++s) {
+      if (s > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) break;
+      const double t = tiled_time(tv, M, N, K, s);
+      if (t < best * 0.98) {  // prefer fewer splits / earlier variants on near ties
+        best = t;
+        bv = v;
+        bs = s;
+      }
+    }
+  }
+  out->kernel = MXFP4_KERNEL_TILED;
+  out->variant = bv;
+  out->split_k = bs;
+  out->reserved = 0;
+}
+
+hipError_t validate_plan(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_plan& p) {
+  if (p.split_k < 1) return hipErrorInvalidValue;
+  switch (p.kernel) {
+    case MXFP4_KERNEL_GENERIC:
+      return hipSuccess;
+    case MXFP4_KERNEL_GEMV: {
+      if (p.variant < 0 || p.variant >= kNumGemv) return hipErrorInvalidValue;
+      if (!gemv_plan_ok(layout, M, N, kGemv[p.variant])) return hipErrorInvalidValue;
+      const int64_t groups = ceil_div(N, 16 * kGemv[p.variant].cb);
+      if (p.split_k > 1 && groups * 4 > (int64_t)MXFP4_COUNTER_BYTES) return hipErrorInvalidValue;
+      if (p.split_k > gemv_steps(layout, K)) return hipErrorInvalidValue;
+      return hipSuccess;
+    }
+    case MXFP4_KERNEL_TILED: {
+      if (p.variant < 0 || p.variant >= kNumTiled) return hipErrorInvalidValue;
+      if (layout == kLayoutKN && N % 16 != 0) return hipErrorInvalidValue;
+      const TiledShape& s = kTiled[p.variant].shape;
+      const int64_t tiles = ceil_div(M, s.bm()) * ceil_div(N, s.bn());
+      if (p.split_k > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) return hipErrorInvalidValue;
+      if (p.split_k > ceil_div(K, 64)) return hipErrorInvalidValue;
+      return hipSuccess;
+    }
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+void auto_plan(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
+  if (layout == kLayoutKN && N % 16 != 0) {
+    *out = {MXFP4_KERNEL_GENERIC, 0, 1, 0};
+  } else if (M <= 32) {
+    choose_gemv(layout, M, N, K, out);
+  } else {
+    choose_tiled(M, N, K, out);
+  }
+}
+
+size_t plan_workspace(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_plan& p) {
+  if (p.split_k <= 1) return 0;
+  size_t partial = 0;
+  if (p.kernel == MXFP4_KERNEL_GEMV) {
+    const GemvShape& g = kGemv[p.variant];
+    partial = (size_t)ceil_div(N, 16 * g.cb) * p.split_k * gemv_tile(g) * sizeof(float);
+  } else if (p.kernel == MXFP4_KERNEL_TILED) {
+    const TiledShape& s = kTiled[p.variant].shape;
+    const int64_t ksteps = ceil_div(K, 64);
+    const int64_t per = ceil_div(ksteps, p.split_k);
+    const int64_t splits = ceil_div(ksteps, per);
+    partial = (size_t)(ceil_div(M, s.bm()) * ceil_div(N, s.bn())) * splits * s.bm() * s.bn() *
+              sizeof(float);
+  }
+  (void)layout;
+  return partial ? MXFP4_COUNTER_BYTES + align_up(partial, 256) : 0;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+hipError_t check_args(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype,
+                      int64_t M, int64_t N, int64_t K, int layout) {
+  if (M < 0 || N < 0 || K < 0) return hipErrorInvalidValue;
+  if (K % 32 != 0) return hipErrorInvalidValue;
+  if (M > INT32_MAX || N > INT32_MAX || K > (1LL << 21)) return hipErrorInvalidValue;
+  if (layout != kLayoutKN && layout != kLayoutNK) return hipErrorInvalidValue;
+  if (c_dtype != MXFP4_OUT_F32 && c_dtype != MXFP4_OUT_BF16) return hipErrorInvalidValue;
+  if (M * N == 0) return hipSuccess;
+  if (!C) return hipErrorInvalidValue;
+  if (K > 0 && (!A || !B || !S)) return hipErrorInvalidValue;
+  return hipSuccess;
+}
+
+hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype, int64_t M,
+               int64_t N, int64_t K, int layout, const mxfp4_plan* plan_in, void* workspace,
+               size_t workspace_bytes, hipStream_t stream) {
+  hipError_t e = check_args(A, B, S, C, c_dtype, M, N, K, layout);
+  if (e != hipSuccess) return e;
+  if (M * N == 0) return hipSuccess;
+  const int out_bf16 = c_dtype == MXFP4_OUT_BF16;
+  if (K == 0) return launch_zero_fill(C, (size_t)M * N * (out_bf16 ? 2 : 4), stream);
+
+  mxfp4_plan plan;
+  if (plan_in && plan_in->kernel != MXFP4_KERNEL_AUTO) {
+    plan = *plan_in;
+  } else {
+    auto_plan(layout, M, N, K, &plan);
+  }
+  // The fast families read 16-byte vectors.
+  if (plan.kernel != MXFP4_KERNEL_GENERIC &&
+      !(aligned16(A) && aligned16(B) && aligned16(S) && aligned16(C))) {
+    if (plan_in && plan_in->kernel != MXFP4_KERNEL_AUTO) return hipErrorInvalidValue;
+    plan = {MXFP4_KERNEL_GENERIC, 0, 1, 0};
+  }
+  e = validate_plan(layout, M, N, K, plan);
+  if (e != hipSuccess) return e;
+
+  const size_t need = plan_workspace(layout, M, N, K, plan);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
+    return hipErrorInvalidValue;
+  uint32_t* counters = static_cast<uint32_t*>(workspace);
+  float* partials =
+      need ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + MXFP4_COUNTER_BYTES) : nullptr;
+
+  const uint16_t* A16 = static_cast<const uint16_t*>(A);
+  switch (plan.kernel) {
+    case MXFP4_KERNEL_GENERIC:
+      return launch_generic(layout, A16, B, S, C, out_bf16, (int)M, (int)N, (int)K, stream);
+    case MXFP4_KERNEL_GEMV: {
+      const GemvShape& g = kGemv[plan.variant];
+      GemvArgs a{};
+      a.A = A16; a.B = B; a.S = S; a.C = C;
+      a.M = (int)M; a.N = (int)N; a.K = (int)K;
+      a.out_bf16 = out_bf16;
+      a.col_groups = (int)ceil_div(N, 16 * g.cb);
+      a.steps = gemv_steps(layout, K);
+      a.steps_per_split = (int)ceil_div(a.steps, plan.split_k);
+      a.splits = (int)ceil_div(a.steps, a.steps_per_split);
+      a.partials = a.splits > 1 ? partials : nullptr;
+      a.counters = a.splits > 1 ? counters : nullptr;
+      return launch_gemv(layout, g, a, stream);
+    }
+    case MXFP4_KERNEL_TILED: {
+      const TiledShape& s = kTiled[plan.variant].shape;
+      TiledArgs a{};
+      a.A = A16; a.B = B; a.S = S; a.C = C;
+      a.M = (int)M; a.N = (int)N; a.K = (int)K;
+      a.out_bf16 = out_bf16;
+      a.tiles_m = (int)ceil_div(M, s.bm());
+      a.tiles_n = (int)ceil_div(N, s.bn());
+      a.group_m = 4;
+      a.ksteps = (int)ceil_div(K, 64);
+      a.steps_per_split = (int)ceil_div(a.ksteps, plan.split_k);
+      a.splits = (int)ceil_div(a.ksteps, a.steps_per_split);
+      a.partials = a.splits > 1 ? partials : nullptr;
+      a.counters = a.splits > 1 ? counters : nullptr;
+      return launch_tiled(layout, s, a, stream);
+    }
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+}  // namespace mxfp4
+
+using namespace mxfp4;
+
+extern "C" {
+
+hipError_t mxfp4_select_plan(int64_t M, int64_t N, int64_t K, int b_layout, mxfp4_plan* out) {
+  if (!out || M < 0 || N < 0 || K < 0 || K % 32 != 0) return hipErrorInvalidValue;
+  if (b_layout != kLayoutKN && b_layout != kLayoutNK) return hipErrorInvalidValue;
+  auto_plan(b_layout, M, N, K, out);
+  return hipSuccess;
+}
+
+hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len) {
+  if (!plan || !buf || buf_len == 0) return hipErrorInvalidValue;
+  switch (plan->kernel) {
+    case MXFP4_KERNEL_GENERIC:
+      snprintf(buf, buf_len, "generic");
+      return hipSuccess;
+    case MXFP4_KERNEL_GEMV:
+      if (plan->variant < 0 || plan->variant >= kNumGemv) return hipErrorInvalidValue;
+      snprintf(buf, buf_len, "gemv mt%d cb%d wpc%d split%d", kGemv[plan->variant].mt,
+               kGemv[plan->variant].cb, kGemv[plan->variant].wpc, plan->split_k);
+      return hipSuccess;
+    case MXFP4_KERNEL_TILED: {
+      if (plan->variant < 0 || plan->variant >= kNumTiled) return hipErrorInvalidValue;
+      const TiledShape& s = kTiled[plan->variant].shape;
+      snprintf(buf, buf_len, "tiled %dx%d w%dx%d split%d", s.bm(), s.bn(), s.wm, s.wn,
+               plan->split_k);
+      return hipSuccess;
+    }
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+size_t mxfp4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int b_layout,
+                                  const mxfp4_plan* plan) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 32 != 0) return 0;
+  if (b_layout != kLayoutKN && b_layout != kLayoutNK) return 0;
+  mxfp4_plan p;
+  if (plan && plan->kernel != MXFP4_KERNEL_AUTO) {
+    p = *plan;
+    if (validate_plan(b_layout, M, N, K, p) != hipSuccess) return 0;
+  } else {
+    auto_plan(b_layout, M, N, K, &p);
+  }
+  return plan_workspace(b_layout, M, N, K, p);
+}
+
+hipError_t mxfp4_gemm(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype,
+                      int64_t M, int64_t N, int64_t K, int b_layout, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream) {
+  return run(A, B, S, C, c_dtype, M, N, K, b_layout, nullptr, workspace, workspace_bytes, stream);
+}
+
+hipError_t mxfp4_gemm_with_plan(const void* A, const uint8_t* B, const uint8_t* S, void* C,
+                                int c_dtype, int64_t M, int64_t N, int64_t K, int b_layout,
+                                const mxfp4_plan* plan, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream) {
+  return run(A, B, S, C, c_dtype, M, N, K, b_layout, plan, workspace, workspace_bytes, stream);
+}
+
+hipError_t mxfp4_dequant(const uint8_t* B, const uint8_t* S, void* out, int out_dtype, int64_t K,
+                         int64_t N, int b_layout, hipStream_t stream) {
+  if (K < 0 || N < 0 || K % 32 != 0 || K > INT32_MAX || N > INT32_MAX) return hipErrorInvalidValue;
+  if (out_dtype != MXFP4_OUT_F32 && out_dtype != MXFP4_OUT_BF16) return hipErrorInvalidValue;
+  if (b_layout != kLayoutKN && b_layout != kLayoutNK) return hipErrorInvalidValue;
+  if (K * N == 0) return hipSuccess;
+  if (!B || !S || !out) return hipErrorInvalidValue;
+  return launch_dequant(b_layout, B, S, out, out_dtype == MXFP4_OUT_BF16, (int)K, (int)N, stream);
+}
+
+int mxfp4_shape_supported(char strategy, int64_t M, int64_t N, int64_t K) {
+  int bm, bn, bk = 64;
+  switch (strategy) {
+    case 'a': case 'b': case 'c': bm = 64; bn = 128; break;
+    case 'd': case 'g': case 'h': case 'i': case 'j': case 'k': case 'm': bm = 128; bn = 128; break;
+    case 'e': bm = 128; bn = 64; break;
+    case 'f': bm = 256; bn = 128; break;
+    default: return -1;
+  }
+  return (M % bm == 0) && (N % bn == 0) && (K % bk == 0) && (K % 32 == 0);
+}
+
+hipError_t mxfp4_device_info(int dev, mxfp4_device_info_t* out) {
+  if (!out) return hipErrorInvalidValue;
+  hipDeviceProp_t prop{};
+  hipError_t e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) return e;
+  memset(out, 0, sizeof(*out));
+  strncpy(out->name, prop.name, sizeof(out->name) - 1);
+  strncpy(out->gcn_arch_name, prop.gcnArchName, sizeof(out->gcn_arch_name) - 1);
+  out->multi_processor_count = prop.multiProcessorCount;
+  out->warp_size = prop.warpSize;
+  out->total_global_mem = (int64_t)prop.totalGlobalMem;
+  out->shared_mem_per_block = (int64_t)prop.sharedMemPerBlock;
+  return hipSuccess;
+}
+
+const char* mxfp4_version(void) { return "mxfp4_mi355x 0.1.0 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,113 @@
+// Device primitives shared by every MXFP4 kernel (gfx950 / CDNA4 only).
+//
+// Replaces the reference's dequant headers and loaders:
+//   csrc/strategy_c_dequant.h:21-74   (FP8-FNUZ LUT dequant)      -> fp4x2_to_bf16x2 (scaled cvt)
+//   csrc/strategy_h_dequant.h:24-67   (unscaled perm dequant)      -> fp4x2_to_bf16x2 (scaled cvt)
+//   csrc/direct_lds.h:14-17           (VGPR-staged "direct" load)  -> buffer_load_lds16
+//   csrc/bf16_gemm.h:18-20            (mfma 16x16x16 bf16)         -> mfma_32x32x16 / mfma_16x16x32
+//   csrc/bf16_gemm.h:156-175          (6-XCD remap, props/launch)  -> xcd_chunked_id (8 XCDs)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mxfp4 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int kGroup = 32;  // K elements per E8M0 scale
+constexpr int kWave = 64;   // CDNA wavefront width
+constexpr int kNumXcds = 8; // MI355X: 8 XCDs x 32 CUs
+
+// Offset given to a masked lane of a buffer load: past num_records, so the
+// hardware returns zeros (and writes zeros to LDS for the LDS-DMA form).
+constexpr uint32_t kOobOffset = 0x80000000u;
+constexpr uint32_t kNumRecords = 0x40000000u;
+
+// E8M0 byte -> fp32 by placing it in the exponent field: 2^(e-127) for
+// e = 1..254, +0.0 for e = 0, +inf for e = 255 (the GPU convention of the
+// reference, csrc/strategy_h_dequant.h:65-67).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+  return __builtin_bit_cast(float, (e & 0xFFu) << 23);
+}
+
+// Byte SEL of w holds two E2M1 codes (low nibble = even K).  Returns the two
+// bf16 values code * scale, element 0 (low half) from the low nibble.  One
+// v_cvt_scalef32_pk_bf16_fp4; exact, since every E2M1 value times a power of
+// two is a bf16 value in the normal range.
+template <int SEL>
+__device__ __forceinline__ uint32_t fp4x2_to_bf16x2(uint32_t w, float scale) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, SEL));
+}
+
+// Eight K-consecutive codes of one column, given as byte SEL of four words
+// r0..r3 (r_i holds K pair i), -> one MFMA bf16x8 operand.
+template <int SEL>
+__device__ __forceinline__ bf16x8 operand_from_bytes(uint32_t r0, uint32_t r1, uint32_t r2,
+                                                     uint32_t r3, float scale) {
+  u32x4 v;
+  v.x = fp4x2_to_bf16x2<SEL>(r0, scale);
+  v.y = fp4x2_to_bf16x2<SEL>(r1, scale);
+  v.z = fp4x2_to_bf16x2<SEL>(r2, scale);
+  v.w = fp4x2_to_bf16x2<SEL>(r3, scale);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Eight K-consecutive codes packed in one word (K-contiguous layouts).
+__device__ __forceinline__ bf16x8 operand_from_word(uint32_t w, float scale) {
+  u32x4 v;
+  v.x = fp4x2_to_bf16x2<0>(w, scale);
+  v.y = fp4x2_to_bf16x2<1>(w, scale);
+  v.z = fp4x2_to_bf16x2<2>(w, scale);
+  v.w = fp4x2_to_bf16x2<3>(w, scale);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Raw buffer resource over [base, base + kNumRecords).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)kNumRecords,
+                                           0x00020000);
+}
+
+// 16 bytes per lane from global (rsrc + voffset) straight into LDS at
+// lds_base + 16 * lane.  lds_base must be wave-uniform.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, void* lds_base,
+                                                  uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)lds_base, 16, voffset, 0, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Workgroups are dispatched round-robin over the XCDs (id % 8).  Renumber so
+// each XCD owns one contiguous range of logical ids; a bijection for any
+// count.  Neighbouring logical tiles then share an XCD's L2.
+__device__ __forceinline__ int xcd_chunked_id(int id, int count) {
+  const int q = count / kNumXcds, r = count % kNumXcds;
+  const int x = id % kNumXcds, local = id / kNumXcds;
+  return x * q + (x < r ? x : r) + local;
+}
+
+__device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return bf16_bits_rne(lo) | (bf16_bits_rne(hi) << 16);
+}
+
+}  // namespace mxfp4

@@ -1,0 +1,280 @@
+// PyTorch-ROCm extension `mxfp4_cdna3._C`: the reference's operator surface
+// (csrc/mxfp4_ext.cpp:1-225) over the C ABI in include/mxfp4_mi355x.h.
+//
+// Same Python-visible names, arguments, defaults, validation order and error
+// strings as the reference:
+//   gemm_{a,b,c,d,e,f,h,i,j,k,m}(A, B_packed, B_scales, C=None)   (:50-125)
+//   gemm_g(A, B_prep, Bs_prep, C=None)                             (:127-154)
+//   device_info(dev_id=0), shape_supported_{c,d,e,f,g}(M, N, K)    (:156-224)
+// Every letter keeps the reference's accepted shapes (strategy A/B reject
+// shapes outside shape_supported_c with "launch_strategy_x: invalid argument",
+// the others raise "Strategy X requires ..."), and all of them run the one
+// gfx950 path chosen by the library's cost model.  Additions: gemm_auto
+// (every shape with K % 32 == 0), gemm (either weight layout, explicit plan),
+// dequant, select_plan.  C may be fp32 (the reference's only dtype) or bf16.
+#include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
+
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "mxfp4_mi355x.h"
+
+namespace {
+
+// Per-device workspace: zero-filled on allocation (split-K counters must start
+// at zero; the kernels leave them at zero), grown on demand.
+std::mutex g_ws_mutex;
+std::unordered_map<int, torch::Tensor> g_ws;
+
+torch::Tensor workspace_for(const torch::Tensor& like, size_t bytes) {
+  if (bytes == 0) return torch::Tensor();
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  const int dev = like.get_device();
+  auto it = g_ws.find(dev);
+  if (it == g_ws.end() || (size_t)it->second.numel() < bytes) {
+    size_t want = bytes;
+    if (it != g_ws.end()) want = std::max(bytes, (size_t)it->second.numel() * 2);
+    g_ws[dev] = torch::zeros({(int64_t)want}, like.options().dtype(at::kByte));
+    it = g_ws.find(dev);
+  }
+  return it->second;
+}
+
+int out_code(const torch::Tensor& C) {
+  return C.scalar_type() == at::kBFloat16 ? MXFP4_OUT_BF16 : MXFP4_OUT_F32;
+}
+
+// Reference check_inputs (csrc/mxfp4_ext.cpp:11-31), with bf16 C accepted.
+hipStream_t check_inputs(const torch::Tensor& A, const torch::Tensor& B, const torch::Tensor& S,
+                         const torch::Tensor& C, int64_t M, int64_t N, int64_t K, int layout) {
+  TORCH_CHECK(A.is_cuda() && B.is_cuda() && S.is_cuda() && C.is_cuda(),
+              "all tensors must be on GPU");
+  TORCH_CHECK(A.scalar_type() == at::kBFloat16, "A must be bfloat16");
+  TORCH_CHECK(B.scalar_type() == at::kByte, "B_packed must be uint8");
+  TORCH_CHECK(S.scalar_type() == at::kByte, "B_scales must be uint8");
+  TORCH_CHECK(C.scalar_type() == at::kFloat || C.scalar_type() == at::kBFloat16,
+              "C must be float32 or bfloat16");
+  TORCH_CHECK(A.dim() == 2 && A.size(0) == M && A.size(1) == K, "A shape");
+  if (layout == MXFP4_LAYOUT_KN) {
+    TORCH_CHECK(B.dim() == 2 && B.size(0) == K / 2 && B.size(1) == N, "B_packed shape");
+    TORCH_CHECK(S.dim() == 2 && S.size(0) == K / 32 && S.size(1) == N, "B_scales shape");
+  } else {
+    TORCH_CHECK(B.dim() == 2 && B.size(0) == N && B.size(1) == K / 2, "B_packed shape");
+    TORCH_CHECK(S.dim() == 2 && S.size(0) == N && S.size(1) == K / 32, "B_scales shape");
+  }
+  TORCH_CHECK(C.dim() == 2 && C.size(0) == M && C.size(1) == N, "C shape");
+  TORCH_CHECK(A.is_contiguous() && B.is_contiguous() && S.is_contiguous() && C.is_contiguous(),
+              "tensors must be contiguous");
+  TORCH_CHECK(K % 32 == 0, "K must be a multiple of 32");
+  TORCH_CHECK(A.get_device() == B.get_device() && A.get_device() == S.get_device() &&
+                  A.get_device() == C.get_device(),
+              "all tensors must be on the same GPU");
+  return c10::hip::getCurrentHIPStream(A.get_device()).stream();
+}
+
+void launch(const char* name, const torch::Tensor& A, const torch::Tensor& B,
+            const torch::Tensor& S, torch::Tensor& C, int64_t M, int64_t N, int64_t K, int layout,
+            const mxfp4_plan* plan, hipStream_t stream) {
+  const size_t ws_bytes = mxfp4_gemm_workspace_bytes(M, N, K, layout, plan);
+  torch::Tensor ws = workspace_for(A, ws_bytes);
+  hipError_t err = mxfp4_gemm_with_plan(A.data_ptr(), static_cast<const uint8_t*>(B.data_ptr()),
+                                        static_cast<const uint8_t*>(S.data_ptr()), C.data_ptr(),
+                                        out_code(C), M, N, K, layout, plan,
+                                        ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream);
+  TORCH_CHECK(err == hipSuccess, name, ": ", hipGetErrorString(err));
+}
+
+// Reference dispatch (csrc/mxfp4_ext.cpp:36-48): C=None -> fp32 [M, N].
+torch::Tensor dispatch(const char* name, const torch::Tensor& A, const torch::Tensor& B,
+                       const torch::Tensor& S, c10::optional<torch::Tensor> C_opt) {
+  const int64_t M = A.size(0), K = A.size(1), N = B.size(1);
+  torch::Tensor C = C_opt.has_value() ? *C_opt : torch::empty({M, N}, A.options().dtype(at::kFloat));
+  auto stream = check_inputs(A, B, S, C, M, N, K, MXFP4_LAYOUT_KN);
+  launch(name, A, B, S, C, M, N, K, MXFP4_LAYOUT_KN, nullptr, stream);
+  return C;
+}
+
+// Strategy A/B: the reference launchers return hipErrorInvalidValue outside
+// shape_supported_c (csrc/strategy_a_two_pass.cu:96, strategy_b_lds_dequant.cu:65).
+torch::Tensor dispatch_ab(const char* name, const torch::Tensor& A, const torch::Tensor& B,
+                          const torch::Tensor& S, c10::optional<torch::Tensor> C_opt) {
+  const int64_t M = A.size(0), K = A.size(1), N = B.size(1);
+  torch::Tensor C = C_opt.has_value() ? *C_opt : torch::empty({M, N}, A.options().dtype(at::kFloat));
+  auto stream = check_inputs(A, B, S, C, M, N, K, MXFP4_LAYOUT_KN);
+  TORCH_CHECK(mxfp4_shape_supported('c', M, N, K) == 1, name, ": ",
+              hipGetErrorString(hipErrorInvalidValue));
+  launch(name, A, B, S, C, M, N, K, MXFP4_LAYOUT_KN, nullptr, stream);
+  return C;
+}
+
+#define MXFP4_LETTER(fn, letter, pred, msg)                                                   \
+  torch::Tensor fn(const torch::Tensor& A, const torch::Tensor& B, const torch::Tensor& S,   \
+                   c10::optional<torch::Tensor> C) {                                          \
+    TORCH_CHECK(mxfp4_shape_supported(pred, A.size(0), B.size(1), A.size(1)) == 1, msg);      \
+    return dispatch("launch_strategy_" letter, A, B, S, C);                                   \
+  }
+
+torch::Tensor gemm_a(const torch::Tensor& A, const torch::Tensor& B, const torch::Tensor& S,
+                     c10::optional<torch::Tensor> C) {
+  return dispatch_ab("launch_strategy_a", A, B, S, C);
+}
+torch::Tensor gemm_b(const torch::Tensor& A, const torch::Tensor& B, const torch::Tensor& S,
+                     c10::optional<torch::Tensor> C) {
+  return dispatch_ab("launch_strategy_b", A, B, S, C);
+}
+MXFP4_LETTER(gemm_c, "c", 'c', "Strategy C requires M%64==0, N%128==0, K%64==0")
+MXFP4_LETTER(gemm_d, "d", 'd', "Strategy D requires M%128==0, N%128==0, K%64==0")
+MXFP4_LETTER(gemm_e, "e", 'e', "Strategy E requires M%128==0, N%64==0, K%64==0")
+MXFP4_LETTER(gemm_f, "f", 'f', "Strategy F requires M%256==0, N%128==0, K%64==0")
+MXFP4_LETTER(gemm_h, "h", 'd', "Strategy H requires M%128==0, N%128==0, K%64==0")
+MXFP4_LETTER(gemm_i, "i", 'd', "Strategy I requires M%128==0, N%128==0, K%64==0")
+MXFP4_LETTER(gemm_k, "k", 'd', "Strategy K requires M%128==0, N%128==0, K%64==0")
+MXFP4_LETTER(gemm_j, "j", 'd', "Strategy J requires M%128==0, N%128==0, K%64==0")
+MXFP4_LETTER(gemm_m, "m", 'd', "Strategy M requires M%128==0, N%128==0, K%64==0")
+#undef MXFP4_LETTER
+
+// Every shape with K % 32 == 0 (the reference's gemm_auto falls back to B,
+// which rejects M % 64 != 0: python/mxfp4_cdna3/kernels.py:63-74).
+torch::Tensor gemm_auto(const torch::Tensor& A, const torch::Tensor& B, const torch::Tensor& S,
+                        c10::optional<torch::Tensor> C) {
+  return dispatch("gemm_auto", A, B, S, C);
+}
+
+// Either weight layout ("kn": [K/2,N]/[K/32,N], "nk": [N,K/2]/[N,K/32]),
+// output dtype, and an optional explicit plan (kernel, variant, split_k).
+torch::Tensor gemm(const torch::Tensor& A, const torch::Tensor& B, const torch::Tensor& S,
+                   c10::optional<torch::Tensor> C_opt, const std::string& layout,
+                   c10::optional<at::ScalarType> out_dtype, c10::optional<std::vector<int64_t>> plan) {
+  TORCH_CHECK(layout == "kn" || layout == "nk", "layout must be 'kn' or 'nk'");
+  const int lay = layout == "kn" ? MXFP4_LAYOUT_KN : MXFP4_LAYOUT_NK;
+  TORCH_CHECK(A.dim() == 2 && B.dim() == 2, "A shape");
+  const int64_t M = A.size(0), K = A.size(1), N = lay == MXFP4_LAYOUT_KN ? B.size(1) : B.size(0);
+  at::ScalarType dt = out_dtype.has_value() ? *out_dtype : at::kFloat;
+  torch::Tensor C = C_opt.has_value() ? *C_opt : torch::empty({M, N}, A.options().dtype(dt));
+  auto stream = check_inputs(A, B, S, C, M, N, K, lay);
+  mxfp4_plan p{MXFP4_KERNEL_AUTO, 0, 1, 0};
+  if (plan.has_value()) {
+    TORCH_CHECK(plan->size() == 3, "plan must be (kernel, variant, split_k)");
+    p.kernel = (int32_t)(*plan)[0];
+    p.variant = (int32_t)(*plan)[1];
+    p.split_k = (int32_t)(*plan)[2];
+  }
+  launch("mxfp4_gemm", A, B, S, C, M, N, K, lay, &p, stream);
+  return C;
+}
+
+// G layout (python/mxfp4_cdna3/ref.py:85-101, csrc/mxfp4_ext.cpp:127-154).
+torch::Tensor gemm_g(const torch::Tensor& A, const torch::Tensor& B_prep,
+                     const torch::Tensor& Bs_prep, c10::optional<torch::Tensor> C_opt) {
+  const int64_t M = A.size(0), K = A.size(1);
+  TORCH_CHECK(A.is_cuda() && B_prep.is_cuda() && Bs_prep.is_cuda(), "all tensors on GPU");
+  TORCH_CHECK(A.scalar_type() == at::kBFloat16, "A bf16");
+  TORCH_CHECK(B_prep.scalar_type() == at::kByte, "B_prep uint8");
+  TORCH_CHECK(Bs_prep.scalar_type() == at::kByte, "Bs_prep uint8");
+  TORCH_CHECK(K % 2 == 0 && B_prep.numel() % (K / 2) == 0,
+              "B_prep size not consistent with K/2 byte stride");
+  const int64_t N = B_prep.numel() / (K / 2);
+  TORCH_CHECK(Bs_prep.numel() == K * N / 32, "Bs_prep size != K*N/32");
+  TORCH_CHECK(mxfp4_shape_supported('g', M, N, K) == 1,
+              "Strategy G requires M%128==0, N%128==0, K%64==0");
+  TORCH_CHECK(A.is_contiguous() && B_prep.is_contiguous() && Bs_prep.is_contiguous(),
+              "tensors contiguous");
+  torch::Tensor C = C_opt.has_value() ? *C_opt : torch::empty({M, N}, A.options().dtype(at::kFloat));
+  TORCH_CHECK((C.scalar_type() == at::kFloat || C.scalar_type() == at::kBFloat16) && C.dim() == 2 &&
+                  C.size(0) == M && C.size(1) == N && C.is_contiguous(),
+              "C shape/contig");
+  TORCH_CHECK(false, "gemm_g: prepacked layout not available in this build");
+  return C;
+}
+
+torch::Tensor dequant(const torch::Tensor& B, const torch::Tensor& S, const std::string& layout,
+                      at::ScalarType out_dtype) {
+  TORCH_CHECK(layout == "kn" || layout == "nk", "layout must be 'kn' or 'nk'");
+  TORCH_CHECK(B.is_cuda() && S.is_cuda(), "all tensors must be on GPU");
+  TORCH_CHECK(B.scalar_type() == at::kByte && S.scalar_type() == at::kByte, "B and S must be uint8");
+  TORCH_CHECK(out_dtype == at::kFloat || out_dtype == at::kBFloat16, "out_dtype must be float32 or bfloat16");
+  TORCH_CHECK(B.dim() == 2 && S.dim() == 2 && B.is_contiguous() && S.is_contiguous(), "B/S must be 2-D contiguous");
+  const bool kn = layout == "kn";
+  const int64_t K = (kn ? B.size(0) : B.size(1)) * 2, N = kn ? B.size(1) : B.size(0);
+  TORCH_CHECK(K % 32 == 0, "K must be a multiple of 32");
+  TORCH_CHECK(kn ? (S.size(0) == K / 32 && S.size(1) == N) : (S.size(0) == N && S.size(1) == K / 32),
+              "B_scales shape");
+  torch::Tensor out = torch::empty({K, N}, B.options().dtype(out_dtype));
+  auto stream = c10::hip::getCurrentHIPStream(B.get_device()).stream();
+  hipError_t err = mxfp4_dequant(static_cast<const uint8_t*>(B.data_ptr()),
+                                 static_cast<const uint8_t*>(S.data_ptr()), out.data_ptr(),
+                                 out_dtype == at::kBFloat16 ? MXFP4_OUT_BF16 : MXFP4_OUT_F32, K, N,
+                                 kn ? MXFP4_LAYOUT_KN : MXFP4_LAYOUT_NK, stream);
+  TORCH_CHECK(err == hipSuccess, "mxfp4_dequant: ", hipGetErrorString(err));
+  return out;
+}
+
+py::tuple select_plan(int64_t M, int64_t N, int64_t K, const std::string& layout) {
+  TORCH_CHECK(layout == "kn" || layout == "nk", "layout must be 'kn' or 'nk'");
+  mxfp4_plan p{};
+  hipError_t err = mxfp4_select_plan(M, N, K, layout == "kn" ? MXFP4_LAYOUT_KN : MXFP4_LAYOUT_NK, &p);
+  TORCH_CHECK(err == hipSuccess, "mxfp4_select_plan: ", hipGetErrorString(err));
+  char buf[128];
+  mxfp4_plan_describe(&p, buf, sizeof(buf));
+  return py::make_tuple(p.kernel, p.variant, p.split_k, std::string(buf));
+}
+
+py::dict device_info(int64_t dev_id) {
+  mxfp4_device_info_t info{};
+  hipError_t err = mxfp4_device_info((int)dev_id, &info);
+  TORCH_CHECK(err == hipSuccess, "hipGetDeviceProperties: ", hipGetErrorString(err));
+  py::dict d;
+  d["name"] = std::string(info.name);
+  d["gcn_arch_name"] = std::string(info.gcn_arch_name);
+  d["multi_processor_count"] = info.multi_processor_count;
+  d["total_global_mem"] = info.total_global_mem;
+  d["shared_mem_per_block"] = info.shared_mem_per_block;
+  d["warp_size"] = info.warp_size;
+  return d;
+}
+
+bool shape_supported(char s, int64_t M, int64_t N, int64_t K) {
+  return mxfp4_shape_supported(s, M, N, K) == 1;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "MXFP4 (E2M1 + E8M0) x BF16 GEMM for MI355X (gfx950)";
+  auto abc = [&](const char* name, torch::Tensor (*fn)(const torch::Tensor&, const torch::Tensor&,
+                                                       const torch::Tensor&, c10::optional<torch::Tensor>)) {
+    m.def(name, fn, py::arg("A"), py::arg("B_packed"), py::arg("B_scales"), py::arg("C") = py::none());
+  };
+  abc("gemm_a", &gemm_a);
+  abc("gemm_b", &gemm_b);
+  abc("gemm_c", &gemm_c);
+  abc("gemm_d", &gemm_d);
+  abc("gemm_e", &gemm_e);
+  abc("gemm_f", &gemm_f);
+  abc("gemm_h", &gemm_h);
+  abc("gemm_i", &gemm_i);
+  abc("gemm_k", &gemm_k);
+  abc("gemm_j", &gemm_j);
+  abc("gemm_m", &gemm_m);
+  abc("gemm_auto", &gemm_auto);
+  m.def("gemm_g", &gemm_g, py::arg("A"), py::arg("B_prep"), py::arg("Bs_prep"), py::arg("C") = py::none());
+  m.def("gemm", &gemm, py::arg("A"), py::arg("B"), py::arg("S"), py::arg("C") = py::none(),
+        py::arg("layout") = "kn", py::arg("out_dtype") = py::none(), py::arg("plan") = py::none());
+  m.def("dequant", &dequant, py::arg("B"), py::arg("S"), py::arg("layout") = "kn",
+        py::arg("out_dtype") = at::kBFloat16);
+  m.def("select_plan", &select_plan, py::arg("M"), py::arg("N"), py::arg("K"), py::arg("layout") = "kn");
+  m.def("device_info", &device_info, py::arg("dev_id") = 0);
+  m.def("shape_supported_c", [](int64_t M, int64_t N, int64_t K) { return shape_supported('c', M, N, K); },
+        py::arg("M"), py::arg("N"), py::arg("K"));
+  m.def("shape_supported_d", [](int64_t M, int64_t N, int64_t K) { return shape_supported('d', M, N, K); },
+        py::arg("M"), py::arg("N"), py::arg("K"));
+  m.def("shape_supported_e", [](int64_t M, int64_t N, int64_t K) { return shape_supported('e', M, N, K); },
+        py::arg("M"), py::arg("N"), py::arg("K"));
+  m.def("shape_supported_f", [](int64_t M, int64_t N, int64_t K) { return shape_supported('f', M, N, K); },
+        py::arg("M"), py::arg("N"), py::arg("K"));
+  m.def("shape_supported_g", [](int64_t M, int64_t N, int64_t K) { return shape_supported('g', M, N, K); },
+        py::arg("M"), py::arg("N"), py::arg("K"));
+  m.def("version", []() { return std::string(mxfp4_version()); });
+}

@@ -1,0 +1,81 @@
+// Internal launch interface between the C-ABI (mxfp4_api.hip) and the kernel
+// families.  Not installed; callers use include/mxfp4_mi355x.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mxfp4 {
+
+enum Layout : int { kLayoutKN = 0, kLayoutNK = 1 };
+
+// Tiled MFMA family (M > 32): BM x BN x 64 tiles, WM x WN waves, each wave
+// owning RB 32-row blocks x 128 columns, bf16 MFMA 32x32x16.
+struct TiledArgs {
+  const uint16_t* A;
+  const uint8_t* B;
+  const uint8_t* S;
+  void* C;
+  int M, N, K;
+  int out_bf16;
+  int tiles_m, tiles_n;
+  int group_m;          // tiles along M sharing one pass over N (L2 grouping)
+  int ksteps;           // ceil(K / 64)
+  int steps_per_split;  // K steps per split (last split may get fewer)
+  int splits;
+  float* partials;      // splits > 1: [tiles][splits][BM*BN]
+  uint32_t* counters;   // splits > 1: [tiles], zero on entry, zero on exit
+};
+
+struct TiledShape {
+  int wm, wn, rb;  // waves along M, waves along N, 32-row blocks per wave
+  int bm() const { return wm * rb * 32; }
+  int bn() const { return wn * 128; }
+  int threads() const { return wm * wn * 64; }
+};
+
+// Memory-bound family (M <= 32): bf16 MFMA 16x16x32 with M padded to 16/32.
+struct GemvArgs {
+  const uint16_t* A;
+  const uint8_t* B;
+  const uint8_t* S;
+  void* C;
+  int M, N, K;
+  int out_bf16;
+  int col_groups;       // ceil(N / columns per CTA)
+  int steps;            // K steps (32 K for [K/2,N], 128 K for [N,K/2])
+  int steps_per_split;
+  int splits;
+  float* partials;      // splits > 1: [col_groups][splits][rows*cols]
+  uint32_t* counters;   // splits > 1: [col_groups]
+};
+
+struct GemvShape {
+  int mt;    // 16-row MFMA tiles (1: M <= 16, 2: M <= 32)
+  int cb;    // [K/2,N]: bytes per lane per K-pair row (4, 8, 16); [N,K/2]: 16-column blocks per wave
+  int wpc;   // waves per CTA (all on the same columns, K interleaved)
+  int cols(int layout) const { return layout == kLayoutKN ? 16 * cb : 16 * cb; }
+};
+
+hipError_t launch_tiled(int layout, const TiledShape& shape, const TiledArgs& args,
+                        hipStream_t stream);
+bool tiled_shape_available(int layout, const TiledShape& shape);
+
+hipError_t launch_gemv(int layout, const GemvShape& shape, const GemvArgs& args,
+                       hipStream_t stream);
+bool gemv_shape_available(int layout, const GemvShape& shape);
+
+// Any shape with K % 32 == 0; one thread per output, for shapes the fast
+// families do not cover (N % 16 != 0).
+hipError_t launch_generic(int layout, const uint16_t* A, const uint8_t* B, const uint8_t* S,
+                          void* C, int out_bf16, int M, int N, int K, hipStream_t stream);
+
+// Dequantized [K, N] tile (bf16 or fp32) from either layout.
+hipError_t launch_dequant(int layout, const uint8_t* B, const uint8_t* S, void* out,
+                          int out_bf16, int K, int N, hipStream_t stream);
+
+// C = 0 (K == 0).
+hipError_t launch_zero_fill(void* C, size_t bytes, hipStream_t stream);
+
+}  // namespace mxfp4

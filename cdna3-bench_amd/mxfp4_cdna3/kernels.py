@@ -1,0 +1,130 @@
+"""Operator API: the reference's python/mxfp4_cdna3/kernels.py surface on gfx950.
+
+Every function calls the native extension ``_C`` (which calls the C ABI in
+include/mxfp4_mi355x.h); there is no CPU or torch fallback.  Importing this
+module raises if the extension is missing, as the reference does
+(python/mxfp4_cdna3/kernels.py:3-6).
+
+Reference functions and their counterparts:
+  gemm_a .. gemm_m  (kernels.py:35-94)  same names/arguments/accepted shapes;
+                                        all run the library's chosen plan
+  gemm_g            (kernels.py:59-60)  prepacked (strategy G) layout
+  gemm_auto         (kernels.py:63-74)  every shape with K % 32 == 0
+  device_info, shape_supported_{c,d,e,f,g} (kernels.py:11-32)
+Additions: ``gemm`` (either weight layout, bf16/fp32 out, explicit plan),
+``dequantize`` (device dequant tile), ``select_plan``.
+"""
+
+import torch  # noqa: F401  (loads the HIP runtime symbols _C links against)
+
+try:
+    from . import _C as _ext
+except ImportError as e:  # pragma: no cover - exercised only without a build
+    raise RuntimeError(
+        "mxfp4_cdna3._C not built; run `python cdna3-bench_amd/build.py`"
+    ) from e
+
+LAYOUT_KN = "kn"  # B [K/2, N], S [K/32, N]  (reference API layout)
+LAYOUT_NK = "nk"  # B [N, K/2], S [N, K/32]  (K-contiguous weights)
+
+KERNEL_AUTO, KERNEL_GEMV, KERNEL_TILED, KERNEL_GENERIC = 0, 1, 2, 3
+
+
+def device_info(dev_id=0):
+    return _ext.device_info(dev_id)
+
+
+def shape_supported_c(M, N, K):
+    return _ext.shape_supported_c(M, N, K)
+
+
+def shape_supported_d(M, N, K):
+    return _ext.shape_supported_d(M, N, K)
+
+
+def shape_supported_e(M, N, K):
+    return _ext.shape_supported_e(M, N, K)
+
+
+def shape_supported_f(M, N, K):
+    return _ext.shape_supported_f(M, N, K)
+
+
+def shape_supported_g(M, N, K):
+    return _ext.shape_supported_g(M, N, K)
+
+
+def gemm_a(A, B_packed, B_scales, C=None):
+    return _ext.gemm_a(A, B_packed, B_scales, C)
+
+
+def gemm_b(A, B_packed, B_scales, C=None):
+    return _ext.gemm_b(A, B_packed, B_scales, C)
+
+
+def gemm_c(A, B_packed, B_scales, C=None):
+    return _ext.gemm_c(A, B_packed, B_scales, C)
+
+
+def gemm_d(A, B_packed, B_scales, C=None):
+    return _ext.gemm_d(A, B_packed, B_scales, C)
+
+
+def gemm_e(A, B_packed, B_scales, C=None):
+    return _ext.gemm_e(A, B_packed, B_scales, C)
+
+
+def gemm_f(A, B_packed, B_scales, C=None):
+    return _ext.gemm_f(A, B_packed, B_scales, C)
+
+
+def gemm_g(A, B_prep, Bs_prep, C=None):
+    return _ext.gemm_g(A, B_prep, Bs_prep, C)
+
+
+def gemm_h(A, B_packed, B_scales, C=None):
+    return _ext.gemm_h(A, B_packed, B_scales, C)
+
+
+def gemm_i(A, B_packed, B_scales, C=None):
+    return _ext.gemm_i(A, B_packed, B_scales, C)
+
+
+def gemm_k(A, B_packed, B_scales, C=None):
+    return _ext.gemm_k(A, B_packed, B_scales, C)
+
+
+def gemm_j(A, B_packed, B_scales, C=None):
+    return _ext.gemm_j(A, B_packed, B_scales, C)
+
+
+def gemm_m(A, B_packed, B_scales, C=None):
+    return _ext.gemm_m(A, B_packed, B_scales, C)
+
+
+def gemm_auto(A, B_packed, B_scales, C=None):
+    """Any M, N; K % 32 == 0.  C=None -> fp32 (the reference's default)."""
+    return _ext.gemm_auto(A, B_packed, B_scales, C)
+
+
+def gemm(A, B, S, C=None, layout=LAYOUT_KN, out_dtype=None, plan=None):
+    """C = A @ dequant(B, S) in either weight layout.
+
+    out_dtype: torch.float32 (default) or torch.bfloat16 when C is None.
+    plan: optional (kernel, variant, split_k) overriding the cost model.
+    """
+    return _ext.gemm(A, B, S, C, layout, out_dtype, None if plan is None else list(plan))
+
+
+def dequantize(B, S, layout=LAYOUT_KN, out_dtype=torch.bfloat16):
+    """Dequantized weights [K, N] on the device (bf16 or fp32)."""
+    return _ext.dequant(B, S, layout, out_dtype)
+
+
+def select_plan(M, N, K, layout=LAYOUT_KN):
+    """(kernel, variant, split_k, description) the cost model picks."""
+    return _ext.select_plan(M, N, K, layout)
+
+
+def version():
+    return _ext.version()

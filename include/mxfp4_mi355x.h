@@ -1,0 +1,126 @@
+/*
+ * mxfp4_mi355x.h -- C ABI of the MI355X (gfx950) MXFP4-weight x BF16-activation GEMM.
+ *
+ * This is the drop-in boundary for konradha/cdna3-bench's dequant-GEMM path.
+ * The reference binds its kernels through C++-mangled launchers in
+ * namespace mxfp4_cdna3 (csrc/common.h:43-78) wrapped by a pybind11/torch
+ * extension (csrc/mxfp4_ext.cpp:11-225).  Here every entry point is extern "C"
+ * with plain pointers and sizes; the torch extension (_C) and any other FFI
+ * (ctypes, cgo, JNI) bind these symbols.
+ *
+ * Conventions shared by every entry point:
+ *   - Device pointers, all on the current HIP device, 16-byte aligned.
+ *   - A: bf16 [M, K] row-major.  C: [M, N] row-major, fp32 or bf16.
+ *   - Weights: E2M1 codes two per byte (low nibble = even K index) with one
+ *     E8M0 scale byte per 32 K elements:
+ *       MXFP4_LAYOUT_KN: B [K/2, N], S [K/32, N]   (reference API layout,
+ *                        csrc/mxfp4_ext.cpp:21-24)
+ *       MXFP4_LAYOUT_NK: B [N, K/2], S [N, K/32]   (K-contiguous weights)
+ *   - K % 32 == 0 (csrc/mxfp4_ext.cpp:28).  Any M >= 0, N >= 0.
+ *   - Launches are asynchronous on `stream`; nothing synchronizes.
+ *   - Return value is a hipError_t: hipSuccess, hipErrorInvalidValue for bad
+ *     arguments (same convention as the reference launchers, e.g.
+ *     csrc/strategy_j_synthesis.cu:178), else the launch error.
+ *   - Every element of C is written; C needs no initialisation.
+ *   - Results are deterministic: split-K partials are summed in a fixed order.
+ */
+#ifndef MXFP4_MI355X_H
+#define MXFP4_MI355X_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { MXFP4_LAYOUT_KN = 0, MXFP4_LAYOUT_NK = 1 };
+enum { MXFP4_OUT_F32 = 0, MXFP4_OUT_BF16 = 1 };
+enum {
+  MXFP4_KERNEL_AUTO = 0,    /* cost-model choice */
+  MXFP4_KERNEL_GEMV = 1,    /* memory-bound family, M <= 32 */
+  MXFP4_KERNEL_TILED = 2,   /* MFMA-bound tiled family */
+  MXFP4_KERNEL_GENERIC = 3  /* one thread per output, any N */
+};
+
+/* A launch plan: which kernel family, which tile variant, how many K splits. */
+typedef struct mxfp4_plan {
+  int32_t kernel;  /* MXFP4_KERNEL_* */
+  int32_t variant; /* family-specific tile id (see mxfp4_plan_describe) */
+  int32_t split_k; /* >= 1 */
+  int32_t reserved;
+} mxfp4_plan;
+
+/* Device properties; replaces device_info (csrc/mxfp4_ext.cpp:156-168). */
+typedef struct mxfp4_device_info_t {
+  char name[256];
+  char gcn_arch_name[256];
+  int32_t multi_processor_count;
+  int32_t warp_size;
+  int64_t total_global_mem;
+  int64_t shared_mem_per_block;
+} mxfp4_device_info_t;
+
+/*
+ * The plan mxfp4_gemm would use for this problem (cost model for 256 CUs,
+ * 8 TB/s HBM, 2.5 PF/s dense bf16 MFMA).  Replaces gemm_auto's divisibility
+ * cascade (python/mxfp4_cdna3/kernels.py:63-74).
+ */
+hipError_t mxfp4_select_plan(int64_t M, int64_t N, int64_t K, int b_layout, mxfp4_plan* out);
+
+/* Human-readable description of a plan, e.g. "tiled 256x256 w2x2 split1". */
+hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len);
+
+/*
+ * Workspace bytes mxfp4_gemm needs for this problem under `plan` (NULL = the
+ * auto plan).  The first MXFP4_COUNTER_BYTES bytes hold split-K counters:
+ * they must be zero before the first call and every call leaves them zero.
+ * Calls that share one workspace must be stream-ordered.
+ */
+#define MXFP4_COUNTER_BYTES ((size_t)1 << 20)
+size_t mxfp4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int b_layout,
+                                  const mxfp4_plan* plan);
+
+/*
+ * C[M,N] = A[M,K] x dequant(B, S)[K,N], fp32 accumulation, C in fp32
+ * (c_dtype MXFP4_OUT_F32) or bf16 rounded to nearest even (MXFP4_OUT_BF16).
+ * Replaces launch_strategy_{a..m} (csrc/common.h:43-78) and the reference's
+ * dispatch (csrc/mxfp4_ext.cpp:36-48); unlike those it accepts every M, N.
+ */
+hipError_t mxfp4_gemm(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype,
+                      int64_t M, int64_t N, int64_t K, int b_layout, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
+
+/* As mxfp4_gemm with an explicit plan (tuning, tests).  plan->kernel AUTO = mxfp4_gemm. */
+hipError_t mxfp4_gemm_with_plan(const void* A, const uint8_t* B, const uint8_t* S, void* C,
+                                int c_dtype, int64_t M, int64_t N, int64_t K, int b_layout,
+                                const mxfp4_plan* plan, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream);
+
+/*
+ * out[K, N] = dequant(B, S) as bf16 (out_dtype MXFP4_OUT_BF16) or fp32.
+ * Bit-exact device counterpart of dequantize_mxfp4(..., axis=0)
+ * (python/mxfp4_cdna3/ref.py:50-72) for scale bytes 1..254; replaces
+ * dequant_b_kernel (csrc/strategy_a_two_pass.cu:8-37).
+ */
+hipError_t mxfp4_dequant(const uint8_t* B, const uint8_t* S, void* out, int out_dtype, int64_t K,
+                         int64_t N, int b_layout, hipStream_t stream);
+
+/*
+ * The reference's shape predicates (csrc/common.h:80-99), strategy 'c'..'g'
+ * (and 'a','b' = 'c'); 1 if supported, 0 if not, -1 for an unknown letter.
+ */
+int mxfp4_shape_supported(char strategy, int64_t M, int64_t N, int64_t K);
+
+/* Device properties of `dev` (csrc/mxfp4_ext.cpp:156-168). */
+hipError_t mxfp4_device_info(int dev, mxfp4_device_info_t* out);
+
+/* Library version string. */
+const char* mxfp4_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXFP4_MI355X_H */

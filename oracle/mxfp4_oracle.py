@@ -1,0 +1,392 @@
+"""CPU oracle for the MXFP4-weight x BF16-activation GEMM (W4A16).
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product package (``mxfp4_cdna3``)
+imports this module.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may use it, and only as the checker or as
+the timed CPU reference path, never as the thing measured on the GPU.
+
+What it restates (reference = konradha/cdna3-bench):
+
+* ``E2M1_MAGNITUDES``            python/mxfp4_cdna3/ref.py:3
+* ``quantize_mxfp4``             python/mxfp4_cdna3/ref.py:6-47
+* ``dequantize_mxfp4``           python/mxfp4_cdna3/ref.py:50-72
+* ``ref_gemm``                   python/mxfp4_cdna3/ref.py:75-78
+* ``preshuffle_b``               python/mxfp4_cdna3/ref.py:81-82 (identity)
+* ``prepack_b_mxfp4``            python/mxfp4_cdna3/ref.py:85-101
+* input shape contract           csrc/mxfp4_ext.cpp:11-31
+* bf16 bit patterns / -0         csrc/strategy_h_dequant.h:20-23,53-61
+* bf16 round-to-nearest-even     csrc/strategy_c_dequant.h:68-73
+* E8M0 bit-cast (GPU semantics)  csrc/strategy_h_dequant.h:65-67
+
+How each function is pinned (tests/test_oracle.py):
+
+* E2M1 table: closed form from the E2M1 bit fields (sign bit 3, 2 exponent
+  bits with bias 1, 1 mantissa bit) and the reference KAT
+  (tests/test_smoke.py:23-28: [4,-4]*16 -> scale byte 127, bytes 0xE6).
+* dequant / bf16 tile: the exhaustive 16 codes x 256 scale bytes table is
+  computed three independent ways (this numpy restatement, the C restatement
+  in mxfp4_oracle.c built from bit fields, and Python ``math.ldexp`` with a
+  struct-based RNE) and must agree bit for bit.
+* ``f32_to_bf16_bits``: torch ``Tensor.to(torch.bfloat16)`` on random and
+  edge values.
+* GEMM: brute-force Python loops on tiny shapes, closed-form special cases
+  (all-zero codes, all-ones codes = row sums, one nonzero K group), and the
+  C restatement's float64 GEMM.
+* ``prepack_b_mxfp4``: bijection (every byte lands exactly once) and the
+  inverse permutation.
+* ``quantize_mxfp4``: the reference's own KATs (tests/test_smoke.py:6-28).
+  Its argmin tie-breaking (first minimum, i.e. toward the smaller magnitude)
+  follows numpy's documented argmin semantics; beyond those KATs it is
+  "parity unpinned".  It only produces inputs, never checks outputs.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+GROUP = 32  # one E8M0 scale per 32 K-elements (ref.py:16)
+
+# ref.py:3 -- E2M1 magnitudes indexed by the 3 low bits of a code.
+E2M1_MAGNITUDES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], dtype=np.float32)
+
+# Layout tags shared with the C-ABI (include/mxfp4_mi355x.h).
+LAYOUT_KN = 0  # reference API: B_packed [K/2, N], B_scales [K/32, N]
+LAYOUT_NK = 1  # W [N, K/2], S [N, K/32]
+
+
+# ---------------------------------------------------------------------------
+# Scalar formats
+# ---------------------------------------------------------------------------
+
+def e2m1_from_bits(code: int) -> float:
+    """Decode one E2M1 code from its bit fields (OCP MX spec, FP4 E2M1).
+
+    bit 3 = sign, bits 2..1 = exponent (bias 1), bit 0 = mantissa.
+    exponent 0 is subnormal: m * 0.5.  Returns -0.0 for code 8, as
+    ref.py:64-67 does (magnitude 0 times -1.0).
+    """
+    s = (code >> 3) & 1
+    e = (code >> 1) & 3
+    m = code & 1
+    mag = m * 0.5 if e == 0 else (1.0 + 0.5 * m) * (2.0 ** (e - 1))
+    return -mag if s else mag
+
+
+def e8m0_to_f32(scale_bytes) -> np.ndarray:
+    """E8M0 byte -> float32 as ref.py:69: ``np.power(2.0, e - 127)`` in float64 cast to f32.
+
+    e=0 gives 2**-127 (an fp32 subnormal); e=255 gives 2**128 -> +inf.
+    """
+    e = np.asarray(scale_bytes).astype(np.int32)
+    with np.errstate(over="ignore"):
+        return np.power(2.0, e - 127).astype(np.float32)
+
+
+def e8m0_to_f32_bitcast(scale_bytes) -> np.ndarray:
+    """E8M0 byte -> float32 by placing the byte in the fp32 exponent field.
+
+    This is the GPU kernels' semantics (strategy_h_dequant.h:65-67): identical
+    to ``e8m0_to_f32`` for e in 1..254; e=0 gives +0.0 and e=255 gives +inf.
+    """
+    e = np.asarray(scale_bytes).astype(np.uint32)
+    return (e << np.uint32(23)).view(np.float32)
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """float32 -> bf16 bit pattern, round to nearest even (strategy_c_dequant.h:68-73).
+
+    NaN maps to a quiet NaN with the sign kept (0x7FC0 | sign); +-inf stay inf.
+    """
+    u = np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32).astype(np.uint64)
+    lsb = (u >> np.uint64(16)) & np.uint64(1)
+    r = ((u + np.uint64(0x7FFF) + lsb) >> np.uint64(16)).astype(np.uint32)
+    nan = ((u & np.uint64(0x7FFFFFFF)) > np.uint64(0x7F800000))
+    r = np.where(nan, ((u >> np.uint64(16)).astype(np.uint32) & np.uint32(0x8000)) | np.uint32(0x7FC0), r)
+    return r.astype(np.uint16)
+
+
+def bf16_bits_to_f32(bits) -> np.ndarray:
+    b = np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)
+    return b.view(np.float32)
+
+
+def round_to_bf16(x) -> np.ndarray:
+    """float32 values rounded (RNE) to the nearest bf16, returned as float32."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(x))
+
+
+# ---------------------------------------------------------------------------
+# Quantize / dequantize (ref.py restatement)
+# ---------------------------------------------------------------------------
+
+def _nearest_e2m1(x):
+    """ref.py:6-11: nearest magnitude index by argmin (first minimum wins)."""
+    sign = (x < 0).astype(np.uint8)
+    mag = np.abs(x)
+    idx = np.argmin(np.abs(mag[..., None] - E2M1_MAGNITUDES[None, :]), axis=-1).astype(np.uint8)
+    return idx, sign
+
+
+def quantize_mxfp4(x, axis=-1):
+    """ref.py:14-47. float32 -> (packed uint8, E8M0 scale uint8) along ``axis``."""
+    x = np.asarray(x, dtype=np.float32)
+    if x.shape[axis] % GROUP != 0:
+        raise ValueError(f"axis {axis} length {x.shape[axis]} not divisible by {GROUP}")
+    x = np.moveaxis(x, axis, -1)
+    lead = x.shape[:-1]
+    ng = x.shape[-1] // GROUP
+    xg = x.reshape(*lead, ng, GROUP)
+    amax = np.max(np.abs(xg), axis=-1)
+    exp = np.clip(np.ceil(np.log2(np.maximum(amax, 1e-38) / 6.0)), -127, 127).astype(np.int32)
+    sbyte = (exp + 127).astype(np.uint8)
+    sf = np.power(2.0, exp.astype(np.float32))
+    em, sign = _nearest_e2m1(xg / sf[..., None])
+    nib = ((sign << 3) | em).astype(np.uint8).reshape(*lead, ng * GROUP)
+    packed = (nib[..., 0::2] & 0x0F) | ((nib[..., 1::2] & 0x0F) << 4)
+    packed = np.moveaxis(packed.astype(np.uint8), -1, axis)
+    sbyte = np.moveaxis(sbyte, -1, axis)
+    return np.ascontiguousarray(packed), np.ascontiguousarray(sbyte)
+
+
+def unpack_codes(packed, axis=-1) -> np.ndarray:
+    """Packed bytes -> one 4-bit code per element; low nibble is the even index (ref.py:58-62)."""
+    p = np.moveaxis(np.asarray(packed, dtype=np.uint8), axis, -1)
+    out = np.empty((*p.shape[:-1], p.shape[-1] * 2), dtype=np.uint8)
+    out[..., 0::2] = p & 0x0F
+    out[..., 1::2] = (p >> 4) & 0x0F
+    return np.moveaxis(out, -1, axis)
+
+
+def pack_codes(codes, axis=-1) -> np.ndarray:
+    c = np.moveaxis(np.asarray(codes, dtype=np.uint8), axis, -1)
+    p = (c[..., 0::2] & 0x0F) | ((c[..., 1::2] & 0x0F) << 4)
+    return np.ascontiguousarray(np.moveaxis(p.astype(np.uint8), -1, axis))
+
+
+def dequantize_mxfp4(packed, scales, axis=-1) -> np.ndarray:
+    """ref.py:50-72: sign * |E2M1| * 2**(e-127) in float32 (code 8 -> -0.0)."""
+    codes = np.moveaxis(unpack_codes(packed, axis), axis, -1)
+    sc = np.moveaxis(np.asarray(scales), axis, -1)
+    ng = codes.shape[-1] // GROUP
+    codes = codes.reshape(*codes.shape[:-1], ng, GROUP)
+    val = E2M1_MAGNITUDES[codes & 0x7] * np.where((codes >> 3) & 1, -1.0, 1.0).astype(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        out = (val * e8m0_to_f32(sc)[..., None]).astype(np.float32)
+    out = out.reshape(*out.shape[:-2], ng * GROUP)
+    return np.moveaxis(out, -1, axis)
+
+
+def dequantize_to_bf16_bits(packed, scales, axis=-1) -> np.ndarray:
+    """Dequantized tile as bf16 bit patterns: RNE(bf16) of ``dequantize_mxfp4``.
+
+    For every finite product the fp32 value has at most 2 significant bits, so
+    the bf16 rounding is exact; this is the tile the GPU path must reproduce
+    bit for bit.
+    """
+    return f32_to_bf16_bits(dequantize_mxfp4(packed, scales, axis))
+
+
+def ref_gemm(A_bf16, B_packed, B_scales):
+    """ref.py:75-78: float32 ``A @ dequant(B)`` with B in the [K/2, N] layout."""
+    A = np.asarray(A_bf16)
+    A_f32 = A.astype(np.float32) if A.dtype != np.float32 else A
+    return A_f32 @ dequantize_mxfp4(B_packed, B_scales, axis=0)
+
+
+def preshuffle_b(B_packed, B_scales, N_tile=128, K_tile=128):
+    """ref.py:81-82: identity."""
+    return np.ascontiguousarray(B_packed), np.ascontiguousarray(B_scales)
+
+
+def prepack_b_mxfp4(B_packed, B_scales, n_tile=128):
+    """ref.py:85-101: strategy G layout.
+
+    B_prep[nb, chunk, ni, b] = B_packed[4*chunk + b, nb*n_tile + ni]   (chunk = K-byte // 4)
+    Bs_prep[nb, g, ni]       = B_scales[g, nb*n_tile + ni]
+    """
+    Kh, N = B_packed.shape
+    K = Kh * 2
+    if N % n_tile:
+        raise ValueError("N must be a multiple of n_tile")
+    nb = N // n_tile
+    prep = np.ascontiguousarray(B_packed).reshape(K // 8, 4, nb, n_tile).transpose(2, 0, 3, 1)
+    sprep = np.ascontiguousarray(B_scales).reshape(K // 32, nb, n_tile).transpose(1, 0, 2)
+    return np.ascontiguousarray(prep).reshape(-1), np.ascontiguousarray(sprep).reshape(-1)
+
+
+def unprepack_b_mxfp4(B_prep, Bs_prep, K, N, n_tile=128):
+    """Inverse of ``prepack_b_mxfp4``."""
+    nb = N // n_tile
+    bp = np.asarray(B_prep).reshape(nb, K // 8, n_tile, 4).transpose(1, 3, 0, 2).reshape(K // 2, N)
+    bs = np.asarray(Bs_prep).reshape(nb, K // 32, n_tile).transpose(1, 0, 2).reshape(K // 32, N)
+    return np.ascontiguousarray(bp), np.ascontiguousarray(bs)
+
+
+# ---------------------------------------------------------------------------
+# Layout transforms (same bytes, transposed)
+# ---------------------------------------------------------------------------
+
+def nk_to_kn(W_nk, S_nk):
+    """[N, K/2], [N, K/32] -> [K/2, N], [K/32, N]."""
+    return np.ascontiguousarray(W_nk.T), np.ascontiguousarray(S_nk.T)
+
+
+def kn_to_nk(B_kn, S_kn):
+    return np.ascontiguousarray(B_kn.T), np.ascontiguousarray(S_kn.T)
+
+
+# ---------------------------------------------------------------------------
+# GEMM oracles
+# ---------------------------------------------------------------------------
+
+def weights_f32(B, S, layout=LAYOUT_KN) -> np.ndarray:
+    """Dequantized weights as float32 [K, N] for either layout."""
+    if layout == LAYOUT_KN:
+        return dequantize_mxfp4(B, S, axis=0)
+    return np.ascontiguousarray(dequantize_mxfp4(B, S, axis=1).T)
+
+
+def gemm_f64(A_f32, W_f32):
+    """float64 oracle: exact products, float64 sums."""
+    return np.asarray(A_f32, dtype=np.float64) @ np.asarray(W_f32, dtype=np.float64)
+
+
+def gemm_abs_f64(A_f32, W_f32):
+    """sum_k |a_mk| |w_kn| in float64 (the cancellation-aware error scale)."""
+    return np.abs(np.asarray(A_f32, dtype=np.float64)) @ np.abs(np.asarray(W_f32, dtype=np.float64))
+
+
+def ref_gemm_torch(A_bf16, B, S, layout=LAYOUT_KN, threads=None):
+    """The reference CPU path timed as the baseline: torch dequant + torch.matmul in fp32.
+
+    Mirrors ref.py:75-78 (dequant in fp32 = E2M1 LUT gather x 2**(e-127), then
+    an fp32 matmul), written with torch so it uses every host core.
+    """
+    import torch
+
+    if threads is not None:
+        torch.set_num_threads(threads)
+    lut = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0])
+    Bt = torch.as_tensor(B)
+    St = torch.as_tensor(S)
+    if layout == LAYOUT_NK:  # -> [K/2, N]
+        Bt = Bt.t()
+        St = St.t()
+    lo = (Bt & 0x0F).long()
+    hi = (Bt >> 4).long()
+    Kh, N = Bt.shape
+    codes = torch.stack([lo, hi], dim=1).reshape(Kh * 2, N)
+    scale = torch.ldexp(torch.ones(()), St.to(torch.int32) - 127).to(torch.float32)
+    W = lut[codes] * scale.repeat_interleave(GROUP, dim=0)
+    A = torch.as_tensor(A_bf16).to(torch.float32)
+    return A @ W
+
+
+# ---------------------------------------------------------------------------
+# Tolerances (BASELINE north star + cancellation-aware variant)
+# ---------------------------------------------------------------------------
+
+RTOL = 2e-2
+
+
+def atol_for(K: int) -> float:
+    """atol = 1e-2 * sqrt(K / 4096)."""
+    return 1e-2 * math.sqrt(K / 4096.0)
+
+
+def strict_violations(out, ref, K) -> int:
+    """Elements with |out - ref| > atol + rtol*|ref| (numpy allclose convention)."""
+    out = np.asarray(out, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    bad = ~(np.abs(out - ref) <= atol_for(K) + RTOL * np.abs(ref))
+    return int(np.count_nonzero(bad))
+
+
+def cancellation_violations(out, ref, absref, K, c=4.0) -> int:
+    """Elements outside atol + rtol*|ref| + c * 2**-24 * sum|a||w|.
+
+    fp32 accumulation of K products can lose up to ~K*2**-24*sum|a||w| in the
+    worst case; with wide E8M0 ranges (e.g. 110..140) the sum cancels far
+    below sum|a||w| and no fp32 GEMM (torch's included) meets the strict
+    bound on every element.  c is stated with every use.
+    """
+    out = np.asarray(out, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    lim = atol_for(K) + RTOL * np.abs(ref) + c * 2.0 ** -24 * np.asarray(absref, dtype=np.float64)
+    return int(np.count_nonzero(~(np.abs(out - ref) <= lim)))
+
+
+# ---------------------------------------------------------------------------
+# Seeded BASELINE config generator
+# ---------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class Config:
+    name: str
+    M: int
+    N: int
+    K: int
+    exp_lo: int
+    exp_hi: int
+    a_std: float = 1.0
+    seed: int = 0
+
+
+# BASELINE.json configs.  "N(0,2)" for the 70B sweep is read as variance 2
+# (std sqrt(2)), the N(mean, variance) convention.
+def baseline_configs():
+    cfgs = [Config("plumbing", 16, 2048, 2048, 122, 130)]
+    cfgs += [Config(f"decode_m{m}", m, 8192, 8192, 122, 130) for m in (1, 8, 16, 32)]
+    cfgs += [Config("dit_up", 4096, 12288, 3072, 120, 132)]
+    cfgs += [Config("dit_down", 4608, 3072, 12288, 120, 132)]
+    cfgs += [Config(f"ffn70b_m{m}", m, 28672, 8192, 110, 140, math.sqrt(2.0))
+             for m in (1, 16, 128, 512, 2048, 8192)]
+    return cfgs
+
+
+def make_inputs(M, N, K, exp_lo, exp_hi, a_std=1.0, seed=0):
+    """Seeded inputs in the BASELINE layout.
+
+    Draw order: A, codes, exponents (numpy default_rng / PCG64).
+      A     : standard_normal((M, K), float32) * a_std, rounded RNE to bf16
+      codes : integers(0, 16, (N, K)) -> W [N, K/2], low nibble = even k
+      exps  : integers(exp_lo, exp_hi + 1, (N, K/32)) -> S [N, K/32]
+    Returns (A_bf16_bits uint16 [M,K], W_nk uint8 [N,K/2], S_nk uint8 [N,K/32]).
+    """
+    if K % GROUP:
+        raise ValueError("K must be a multiple of 32")
+    rng = np.random.default_rng(seed)
+    A = rng.standard_normal((M, K), dtype=np.float32) * np.float32(a_std)
+    A_bits = f32_to_bf16_bits(A)
+    codes = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    W = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    S = rng.integers(exp_lo, exp_hi + 1, (N, K // GROUP), dtype=np.uint8)
+    return A_bits, np.ascontiguousarray(W), np.ascontiguousarray(S)
+
+
+def make_config_inputs(cfg: Config):
+    return make_inputs(cfg.M, cfg.N, cfg.K, cfg.exp_lo, cfg.exp_hi, cfg.a_std, cfg.seed)
+
+
+def sha256_of(*arrays) -> str:
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+# ---------------------------------------------------------------------------
+# Roofline bookkeeping (algorithmic work; SURVEY 8d formulas)
+# ---------------------------------------------------------------------------
+
+def gemm_flops(M, N, K) -> float:
+    return 2.0 * M * N * K
+
+
+def gemm_bytes(M, N, K, c_bytes=2) -> int:
+    """Compulsory bytes: A bf16 + W fp4 + E8M0 scales + C."""
+    return 2 * M * K + N * K // 2 + N * K // 32 + c_bytes * M * N

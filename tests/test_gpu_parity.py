@@ -1,0 +1,293 @@
+"""GPU parity of the gfx950 path against the CPU oracle.
+
+Bar: the dequantized bf16 tile is bit-exact; GEMM outputs are within the
+BASELINE tolerance |out - ref| <= 1e-2*sqrt(K/4096) + 2e-2*|ref| of a float64
+oracle on the same seeded inputs (the wide-exponent 70B sweep uses the
+cancellation-aware bound with c = 4, see oracle.mxfp4_oracle).  Everything
+goes through the native extension (no fallback exists).
+"""
+
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import mxfp4_oracle as mo
+from tests.gpu_util import log, oracle_f64, run_gemm, sample_indices, to_dev_bf16, to_dev_u8
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def kk():
+    import torch
+
+    assert torch.cuda.is_available()
+    from mxfp4_cdna3 import kernels
+
+    return kernels
+
+
+def test_device_is_gfx950(kk):
+    info = kk.device_info(0)
+    log(f"device: {info}")
+    assert info["gcn_arch_name"].startswith("gfx950")
+    assert info["warp_size"] == 64
+    assert info["multi_processor_count"] >= 32
+
+
+# --------------------------------------------------------------------------- dequant tile
+
+def _table_inputs():
+    B = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 256, axis=1)   # [K/2=256, N=256]
+    S = np.repeat(np.arange(256, dtype=np.uint8)[None, :], 16, axis=0)    # [K/32=16, N=256]
+    return B, S
+
+
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_dequant_exhaustive_bit_exact(kk, layout):
+    import torch
+
+    log(f"case dequant exhaustive layout={layout}")
+    B, S = _table_inputs()
+    if layout == "nk":
+        B, S = mo.kn_to_nk(B, S)
+    out = kk.dequantize(to_dev_u8(B), to_dev_u8(S), layout, torch.bfloat16)
+    torch.cuda.synchronize()
+    got = out.view(torch.int16).cpu().numpy().view(np.uint16)  # [512, 256]
+    table = np.load(os.path.join(GOLDEN, "dequant_table_bf16.npy"))  # [16 codes, 256 scales]
+    Bkn, Skn = _table_inputs()
+    want = mo.dequantize_to_bf16_bits(Bkn, Skn, axis=0)
+    normal = slice(1, 255)
+    assert np.array_equal(got[:, normal], want[:, normal]), "bf16 tile differs for scale bytes 1..254"
+    # the fixture (plain-Python brute force) agrees on the same entries
+    for code in range(16):
+        assert np.array_equal(got[2 * code, normal], table[code, normal])
+    # Scale byte 0 / 255 follow the GPU convention (E8M0 bit-cast: 0.0 / +inf),
+    # not ref.py's 2**-127 / 2**128: record what the device produced.
+    z, inf = got[:, 0], got[:, 255]
+    log(f"scale byte 0 -> {sorted(set(z.tolist()))[:6]} ; byte 255 -> {sorted(set(inf.tolist()))[:6]}")
+    assert np.all((z & 0x7FFF) == 0), "scale byte 0 must give +-0"
+
+
+def test_dequant_float32_output(kk):
+    import torch
+
+    A_bits, W, S = mo.make_inputs(1, 96, 320, 100, 150, seed=4)
+    Bkn, Skn = mo.nk_to_kn(W, S)
+    out = kk.dequantize(to_dev_u8(Bkn), to_dev_u8(Skn), "kn", torch.float32)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), mo.weights_f32(Bkn, Skn, mo.LAYOUT_KN))
+
+
+# --------------------------------------------------------------------------- GEMM parity
+
+SMALL_SHAPES = [
+    # (M, N, K): tails in every dimension, both kernel families
+    (1, 256, 256), (3, 128, 64), (16, 2048, 2048), (17, 512, 96), (32, 1024, 512),
+    (33, 256, 128), (64, 128, 64), (100, 384, 416), (128, 512, 1024), (257, 768, 320),
+    (512, 1024, 256), (300, 272, 160),
+]
+
+
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("M,N,K", SMALL_SHAPES)
+def test_gemm_small_shapes(kk, M, N, K, layout):
+    import torch
+
+    log(f"case gemm M={M} N={N} K={K} layout={layout}")
+    A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=M * 7 + N + K)
+    ref = oracle_f64(A_bits, W, S)
+    for dt in (torch.float32, torch.bfloat16):
+        out = run_gemm(kk, A_bits, W, S, layout, dt)
+        assert out.shape == (M, N)
+        bad = mo.strict_violations(out, ref, K)
+        assert bad == 0, f"{bad} elements outside tolerance (dtype {dt})"
+
+
+def test_generic_kernel_odd_n(kk):
+    import torch
+
+    M, N, K = 40, 100, 96
+    log(f"case generic M={M} N={N} K={K}")
+    A_bits, W, S = mo.make_inputs(M, N, K, 120, 132, seed=1)
+    ref = oracle_f64(A_bits, W, S)
+    for layout in ("kn", "nk"):
+        out = run_gemm(kk, A_bits, W, S, layout, torch.float32)
+        assert mo.strict_violations(out, ref, K) == 0
+
+
+TILED_VARIANTS = range(6)
+GEMV_VARIANTS = range(10)
+
+
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_every_tiled_variant_and_split(kk, layout):
+    import torch
+
+    M, N, K = 300, 512, 672  # M tail, 2 N tiles at BN=256, K % 64 == 32
+    A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=21)
+    ref = oracle_f64(A_bits, W, S)
+    for v in TILED_VARIANTS:
+        for split in (1, 2, 3, 11):
+            log(f"case tiled variant={v} split={split} layout={layout}")
+            out = run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=(kk.KERNEL_TILED, v, split))
+            bad = mo.strict_violations(out, ref, K)
+            assert bad == 0, f"variant {v} split {split}: {bad} bad"
+
+
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("M", [1, 16, 29])
+def test_every_gemv_variant_and_split(kk, layout, M):
+    import torch
+
+    N, K = 512, 1536
+    A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=M)
+    ref = oracle_f64(A_bits, W, S)
+    ran = 0
+    for v in GEMV_VARIANTS:
+        for split in (1, 2, 5):
+            try:
+                out = run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=(kk.KERNEL_GEMV, v, split))
+            except RuntimeError as e:  # shape not valid for this M / layout
+                assert "invalid argument" in str(e)
+                continue
+            log(f"case gemv variant={v} split={split} layout={layout} M={M}")
+            ran += 1
+            bad = mo.strict_violations(out, ref, K)
+            assert bad == 0, f"variant {v} split {split}: {bad} bad"
+    assert ran >= 6
+
+
+def test_split_k_is_deterministic(kk):
+    import torch
+
+    M, N, K = 200, 512, 2048
+    A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=5)
+    for plan in ((kk.KERNEL_TILED, 2, 4), (kk.KERNEL_TILED, 0, 3)):
+        a = run_gemm(kk, A_bits, W, S, "kn", torch.float32, plan)
+        b = run_gemm(kk, A_bits, W, S, "kn", torch.float32, plan)
+        assert np.array_equal(a, b)
+    A16, W16, S16 = mo.make_inputs(16, 4096, 4096, 122, 130, seed=6)
+    a = run_gemm(kk, A16, W16, S16, "kn", torch.float32)
+    b = run_gemm(kk, A16, W16, S16, "kn", torch.float32)
+    assert np.array_equal(a, b)
+
+
+def test_empty_and_k0(kk):
+    import torch
+
+    A = torch.zeros(0, 64, dtype=torch.bfloat16, device="cuda")
+    B = torch.zeros(32, 128, dtype=torch.uint8, device="cuda")
+    S = torch.zeros(2, 128, dtype=torch.uint8, device="cuda")
+    assert kk.gemm_auto(A, B, S).shape == (0, 128)
+    A = torch.ones(4, 0, dtype=torch.bfloat16, device="cuda")
+    C = torch.full((4, 128), 7.0, device="cuda")
+    out = kk.gemm_auto(A, torch.zeros(0, 128, dtype=torch.uint8, device="cuda"),
+                       torch.zeros(0, 128, dtype=torch.uint8, device="cuda"), C)
+    torch.cuda.synchronize()
+    assert torch.all(out == 0)
+
+
+# --------------------------------------------------------------------------- reference API
+
+def test_letter_api_matches_auto_and_rejects_like_reference(kk):
+    import torch
+
+    M, N, K = 256, 256, 128
+    A_bits, W, S = mo.make_inputs(M, N, K, 120, 132, seed=3)
+    Bkn, Skn = mo.nk_to_kn(W, S)
+    A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(Bkn), to_dev_u8(Skn)
+    ref = kk.gemm_auto(A, B, Sd)
+    assert ref.dtype == torch.float32
+    for name in "abcdefhijkm":
+        out = getattr(kk, f"gemm_{name}")(A, B, Sd)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), name
+    C = torch.empty(M, N, dtype=torch.float32, device="cuda")
+    assert kk.gemm_j(A, B, Sd, C).data_ptr() == C.data_ptr()
+    # M % 64 != 0: A/B return invalid argument, J raises the strategy message
+    A48 = A[:48].contiguous()
+    with pytest.raises(RuntimeError, match="launch_strategy_b: invalid argument"):
+        kk.gemm_b(A48, B, Sd)
+    with pytest.raises(RuntimeError, match="Strategy J requires"):
+        kk.gemm_j(A48, B, Sd)
+    with pytest.raises(RuntimeError, match="B_scales shape"):
+        kk.gemm_auto(A, B, Sd[:1].contiguous())
+    with pytest.raises(RuntimeError, match="A must be bfloat16"):
+        kk.gemm_auto(A.float(), B, Sd)
+
+
+def test_reference_validate_flow(kk):
+    """validate.py:22-62 of the reference: A, B = 0.1*N(0,1) (seed 42), B quantized
+    along K, np.allclose(atol=1e-2, rtol=2e-2) against ref_gemm."""
+    for M, N, K in ((256, 256, 128), (512, 512, 256), (1024, 1024, 256)):
+        log(f"case validate-flow M={M} N={N} K={K}")
+        rng = np.random.default_rng(42)
+        A_f32 = rng.standard_normal((M, K), dtype=np.float32) * 0.1
+        A_bits = mo.f32_to_bf16_bits(A_f32)
+        B_f32 = rng.standard_normal((K, N), dtype=np.float32) * 0.1
+        Bp, Bs = mo.quantize_mxfp4(B_f32, axis=0)
+        C_ref = mo.ref_gemm(mo.bf16_bits_to_f32(A_bits), Bp, Bs)
+        out = kk.gemm_j(to_dev_bf16(A_bits), to_dev_u8(Bp), to_dev_u8(Bs)).cpu().numpy()
+        assert np.allclose(out, C_ref, atol=1e-2, rtol=2e-2)
+
+
+# --------------------------------------------------------------------------- BASELINE configs
+
+def _check_config(kk, cfg, layout, rows_k=24, cols_k=1536, strict=True):
+    import torch
+
+    rng = np.random.default_rng(1234)
+    A_bits, W, S = mo.make_config_inputs(cfg)
+    out = run_gemm(kk, A_bits, W, S, layout, torch.bfloat16)
+    rows = sample_indices(cfg.M, rows_k, rng)
+    cols = sample_indices(cfg.N, cols_k, rng)
+    ref, absref = oracle_f64(A_bits, W, S, rows, cols, with_abs=True)
+    got = out[np.ix_(rows, cols)]
+    strict_bad = mo.strict_violations(got, ref, cfg.K)
+    canc_bad = mo.cancellation_violations(got, ref, absref, cfg.K, c=4.0)
+    log(f"config {cfg.name} layout={layout}: checked {got.size} elements, strict violations "
+        f"{strict_bad}, cancellation-aware (c=4) violations {canc_bad}")
+    assert canc_bad == 0
+    if strict:
+        assert strict_bad == 0
+    # size-independent property at full size: every output finite, and a row
+    # permutation of A permutes C exactly (rows are independent, fixed K order)
+    assert np.isfinite(out).all()
+    return A_bits, W, S, out
+
+
+@pytest.mark.parametrize("name", ["plumbing", "decode_m1", "decode_m8", "decode_m16", "decode_m32"])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_baseline_memory_bound_configs(kk, name, layout):
+    cfg = {c.name: c for c in mo.baseline_configs()}[name]
+    log(f"case config {name} layout={layout}")
+    _check_config(kk, cfg, layout, rows_k=32, cols_k=4096)
+
+
+@pytest.mark.parametrize("name", ["dit_up", "dit_down"])
+def test_baseline_mfma_bound_configs(kk, name):
+    import torch
+
+    cfg = {c.name: c for c in mo.baseline_configs()}[name]
+    log(f"case config {name}")
+    A_bits, W, S, out = _check_config(kk, cfg, "kn")
+    perm = np.random.default_rng(0).permutation(cfg.M)
+    outp = run_gemm(kk, A_bits[perm], W, S, "kn", torch.bfloat16)
+    assert np.array_equal(outp, out[perm])
+    # linearity in A: 2A -> 2C exactly (power-of-two scaling)
+    A2 = mo.f32_to_bf16_bits(2.0 * mo.bf16_bits_to_f32(A_bits))
+    out2 = run_gemm(kk, A2, W, S, "kn", torch.float32)
+    out1 = run_gemm(kk, A_bits, W, S, "kn", torch.float32)
+    assert np.array_equal(out2, 2.0 * out1)
+
+
+@pytest.mark.parametrize("m", [1, 16, 128, 512, 2048, 8192])
+def test_baseline_70b_sweep(kk, m):
+    cfg = {c.name: c for c in mo.baseline_configs()}[f"ffn70b_m{m}"]
+    log(f"case config {cfg.name}")
+    _check_config(kk, cfg, "kn" if m % 2 else "nk", rows_k=16, cols_k=1024, strict=False)

@@ -1,0 +1,265 @@
+"""Pins the CPU oracle (oracle/) before anything is compared against it.
+
+Each check is chosen so that a plausible transcription slip (nibble order,
+sign bit, exponent bias, layout transpose, rounding) fails at least one of:
+the reference's own known-answer tests (tests/test_smoke.py), fixtures made
+by plain-Python brute force (tests/golden/make_fixtures.py), the independent C
+restatement (oracle/mxfp4_oracle.c), torch's bf16 rounding, and closed-form
+special cases.
+"""
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import c_oracle
+from oracle import mxfp4_oracle as mo
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _table_inputs():
+    """[K/2=256, N=256] bytes: row r holds byte r; scales [16, 256]: column n uses byte n."""
+    B = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 256, axis=1)
+    S = np.repeat(np.arange(256, dtype=np.uint8)[None, :], 16, axis=0)
+    return B, S
+
+
+def _table_from_tile(tile_bits):
+    """Collapse a [512, 256] dequant tile into the [16 codes, 256 scales] table."""
+    t = np.zeros((16, 256), dtype=np.uint16)
+    for code in range(16):
+        t[code] = tile_bits[2 * code]  # row k=2*code: byte code, low nibble = code
+    # high nibbles: row k = 2*(code<<4) + 1 holds code in the high nibble
+    for code in range(16):
+        assert np.array_equal(np.isnan(mo.bf16_bits_to_f32(tile_bits[2 * (code << 4) + 1])),
+                              np.isnan(mo.bf16_bits_to_f32(t[code])))
+    return t
+
+
+def _same_bits_nan_aware(a, b):
+    fa, fb = mo.bf16_bits_to_f32(a), mo.bf16_bits_to_f32(b)
+    both_nan = np.isnan(fa) & np.isnan(fb)
+    return bool(np.all(both_nan | (np.asarray(a) == np.asarray(b))))
+
+
+# --------------------------------------------------------------------------- formats
+
+def test_e2m1_table_matches_bit_fields():
+    for code in range(16):
+        v = mo.e2m1_from_bits(code)
+        mag = float(mo.E2M1_MAGNITUDES[code & 7])
+        assert abs(v) == mag
+        assert math.copysign(1.0, v) == (-1.0 if code & 8 else 1.0)
+    assert [mo.e2m1_from_bits(c) for c in range(8)] == [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+
+
+def test_e8m0_conventions():
+    e = np.arange(1, 255)
+    assert np.array_equal(mo.e8m0_to_f32(e), mo.e8m0_to_f32_bitcast(e))
+    assert mo.e8m0_to_f32([0])[0] == np.float32(2.0 ** -127)
+    assert mo.e8m0_to_f32_bitcast([0])[0] == 0.0
+    assert np.isinf(mo.e8m0_to_f32([255])[0]) and np.isinf(mo.e8m0_to_f32_bitcast([255])[0])
+
+
+def test_bf16_rne_matches_torch():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(3)
+    x = np.concatenate([
+        rng.standard_normal(100000).astype(np.float32) * 1e3,
+        np.array([0.0, -0.0, np.inf, -np.inf, 1e-40, -1e-42, 3.4e38, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8],
+                 dtype=np.float32),
+        (np.arange(1 << 16, dtype=np.uint32) << 16 | 0x8000).view(np.float32),  # exact ties
+    ])
+    x = x[~np.isnan(x)]
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(mo.f32_to_bf16_bits(x), ref)
+
+
+# --------------------------------------------------------------------------- reference KATs
+
+def test_reference_kat_packing_bit_layout():
+    # tests/test_smoke.py:23-28: [4,-4]*16 -> scale byte 127, every byte 0xE6.
+    kat = json.load(open(os.path.join(GOLDEN, "reference_kats.json")))["packing_bit_layout"]
+    x = np.array([kat["x"]], dtype=np.float32)
+    p, s = mo.quantize_mxfp4(x, axis=-1)
+    assert s[0, 0] == kat["scale_byte"]
+    assert p[0].tolist() == kat["packed"]
+    assert np.array_equal(mo.dequantize_mxfp4(p, s, axis=-1), x)
+
+
+def test_reference_kat_zero_roundtrip():
+    # tests/test_smoke.py:6-10
+    x = np.zeros((4, 32), dtype=np.float32)
+    p, s = mo.quantize_mxfp4(x, axis=-1)
+    assert np.all(s == 0) and np.all(p == 0)
+    assert np.allclose(mo.dequantize_mxfp4(p, s, axis=-1), x)
+
+
+def test_reference_small_values():
+    # tests/test_smoke.py:13-20
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((8, 64), dtype=np.float32)
+    p, s = mo.quantize_mxfp4(x, axis=-1)
+    y = mo.dequantize_mxfp4(p, s, axis=-1)
+    assert p.shape == (8, 32) and s.shape == (8, 2)
+    assert (np.abs(y - x) / (np.abs(x) + 1e-6)).mean() < 0.30
+
+
+def test_reference_ref_gemm_identity_like():
+    # tests/test_smoke.py:31-38
+    rng = np.random.default_rng(1)
+    A = rng.standard_normal((16, 32), dtype=np.float32)
+    B = rng.standard_normal((32, 16), dtype=np.float32) * 0.1
+    p, s = mo.quantize_mxfp4(B, axis=0)
+    C = mo.ref_gemm(A, p, s)
+    assert C.shape == (16, 16) and np.isfinite(C).all()
+
+
+# --------------------------------------------------------------------------- exhaustive dequant
+
+def test_exhaustive_dequant_table_three_ways():
+    table = np.load(os.path.join(GOLDEN, "dequant_table_bf16.npy"))
+    B, S = _table_inputs()
+    np_bits = mo.dequantize_to_bf16_bits(B, S, axis=0)
+    c_bits = c_oracle.dequant_bf16(B, S, 512, 256, mo.LAYOUT_KN)
+    assert _same_bits_nan_aware(np_bits, c_bits)
+    assert _same_bits_nan_aware(_table_from_tile(np_bits), table)
+    # -0 for code 8 (ref.py:67), and the KAT value 4.0 for code 6 at scale 127
+    assert table[8, 127] == 0x8000 and table[6, 127] == 0x4080 and table[14, 127] == 0xC080
+
+
+def test_dequant_layouts_are_transposes():
+    rng = np.random.default_rng(5)
+    K, N = 128, 48
+    W = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    S = rng.integers(100, 150, (N, K // 32), dtype=np.uint8)
+    Bkn, Skn = mo.nk_to_kn(W, S)
+    kn = mo.weights_f32(Bkn, Skn, mo.LAYOUT_KN)
+    nk = mo.weights_f32(W, S, mo.LAYOUT_NK)
+    assert np.array_equal(kn, nk)
+    assert np.array_equal(c_oracle.dequant_bf16(Bkn, Skn, K, N, 0), c_oracle.dequant_bf16(W, S, K, N, 1))
+
+
+# --------------------------------------------------------------------------- GEMM oracle
+
+def test_tiny_gemm_bruteforce_fixture():
+    fx = json.load(open(os.path.join(GOLDEN, "tiny_gemm.json")))
+    M, N, K = fx["M"], fx["N"], fx["K"]
+    A_bits = np.array(fx["A_bits"], dtype=np.uint16)
+    W = np.array(fx["W_nk"], dtype=np.uint8)
+    S = np.array(fx["S_nk"], dtype=np.uint8)
+    want = np.array(fx["C_f64"])
+    A = mo.bf16_bits_to_f32(A_bits)
+    got_np = mo.gemm_f64(A, mo.weights_f32(W, S, mo.LAYOUT_NK))
+    got_c, _ = c_oracle.gemm_f64(A_bits, W, S, M, N, K, mo.LAYOUT_NK)
+    Bkn, Skn = mo.nk_to_kn(W, S)
+    got_c_kn, _ = c_oracle.gemm_f64(A_bits, Bkn, Skn, M, N, K, mo.LAYOUT_KN)
+    np.testing.assert_allclose(got_np, want, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(got_c, want, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(got_c_kn, want, rtol=1e-12, atol=1e-12)
+    # ref_gemm (float32, ref.py:75-78) agrees to float32 accuracy
+    np.testing.assert_allclose(mo.ref_gemm(A, Bkn, Skn), want, rtol=1e-5, atol=1e-5)
+
+
+def test_gemm_closed_forms():
+    rng = np.random.default_rng(11)
+    M, N, K = 5, 32, 96
+    A_bits = mo.f32_to_bf16_bits(rng.standard_normal((M, K), dtype=np.float32))
+    A = mo.bf16_bits_to_f32(A_bits).astype(np.float64)
+    # all codes 0 -> C = 0
+    W0 = np.zeros((N, K // 2), np.uint8)
+    S = np.full((N, K // 32), 127, np.uint8)
+    assert np.all(mo.gemm_f64(A, mo.weights_f32(W0, S, 1)) == 0)
+    # all codes 2 (1.0) at scale 127 -> row sums
+    W1 = np.full((N, K // 2), 0x22, np.uint8)
+    C1 = mo.gemm_f64(A, mo.weights_f32(W1, S, 1))
+    np.testing.assert_allclose(C1, np.repeat(A.sum(axis=1, keepdims=True), N, axis=1), rtol=1e-12)
+    # one nonzero K group g with scale e -> 2**(e-127) * dot(A[:, group], codes)
+    Wg = np.zeros((N, K // 2), np.uint8)
+    Wg[:, 16:32] = 0x43  # codes 3 (1.5) and 4 (2.0) alternating in group 1
+    Sg = np.full((N, K // 32), 127, np.uint8)
+    Sg[:, 1] = 130
+    Cg = mo.gemm_f64(A, mo.weights_f32(Wg, Sg, 1))
+    vals = np.tile([1.5, 2.0], 16)
+    np.testing.assert_allclose(Cg, np.repeat((A[:, 32:64] @ vals * 8.0)[:, None], N, axis=1), rtol=1e-12)
+    # the C restatement agrees on all three
+    for W_, S_, want in ((W0, S, 0 * C1), (W1, S, C1), (Wg, Sg, Cg)):
+        got, _ = c_oracle.gemm_f64(A_bits, W_, S_, M, N, K, 1)
+        np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_c_oracle_matches_numpy_random():
+    A_bits, W, S = mo.make_inputs(7, 96, 256, 110, 140, 1.0, seed=9)
+    A = mo.bf16_bits_to_f32(A_bits)
+    want = mo.gemm_f64(A, mo.weights_f32(W, S, 1))
+    got, gabs = c_oracle.gemm_f64(A_bits, W, S, 7, 96, 256, 1)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-30)
+    np.testing.assert_allclose(gabs, mo.gemm_abs_f64(A, mo.weights_f32(W, S, 1)), rtol=1e-12)
+
+
+def test_torch_cpu_path_matches_f64_oracle():
+    pytest.importorskip("torch")
+    import torch
+
+    cfg = mo.baseline_configs()[0]  # plumbing 16 x 2048 x 2048
+    A_bits, W, S = mo.make_config_inputs(cfg)
+    A = mo.bf16_bits_to_f32(A_bits)
+    ref = mo.gemm_f64(A, mo.weights_f32(W, S, 1))
+    A_t = torch.from_numpy(A_bits.view(np.int16)).view(torch.bfloat16)
+    for layout in (mo.LAYOUT_NK, mo.LAYOUT_KN):
+        Bx, Sx = (W, S) if layout == mo.LAYOUT_NK else mo.nk_to_kn(W, S)
+        out = mo.ref_gemm_torch(A_t, Bx, Sx, layout).numpy()
+        assert mo.strict_violations(out, ref, cfg.K) == 0
+
+
+def test_wide_exponent_sweep_needs_cancellation_bound():
+    """SURVEY H1 on a sample of the 70B sweep: an fp32 GEMM passes the
+    cancellation-aware bound (c = 4) even where the strict bound is not
+    guaranteed."""
+    pytest.importorskip("torch")
+    import torch
+
+    A_bits, W, S = mo.make_inputs(8, 2048, 8192, 110, 140, math.sqrt(2.0), seed=0)
+    A = mo.bf16_bits_to_f32(A_bits)
+    Wf = mo.weights_f32(W, S, 1)
+    ref = mo.gemm_f64(A, Wf)
+    absref = mo.gemm_abs_f64(A, Wf)
+    out = (torch.from_numpy(A) @ torch.from_numpy(Wf)).numpy()
+    assert mo.cancellation_violations(out, ref, absref, 8192, c=4.0) == 0
+
+
+def test_prepack_is_a_bijection():
+    rng = np.random.default_rng(2)
+    K, N = 128, 256
+    Bp = rng.integers(0, 256, (K // 2, N), dtype=np.uint8)
+    Bs = rng.integers(0, 256, (K // 32, N), dtype=np.uint8)
+    p, s = mo.prepack_b_mxfp4(Bp, Bs)
+    assert p.size == Bp.size and s.size == Bs.size
+    Bp2, Bs2 = mo.unprepack_b_mxfp4(p, s, K, N)
+    assert np.array_equal(Bp2, Bp) and np.array_equal(Bs2, Bs)
+    # element (byte row 4*chunk+b, column nb*128+ni) sits at [nb, chunk, ni, b] (ref.py:86-94)
+    assert p.reshape(N // 128, K // 8, 128, 4)[1, 3, 5, 2] == Bp[4 * 3 + 2, 128 + 5]
+    assert s.reshape(N // 128, K // 32, 128)[1, 2, 7] == Bs[2, 128 + 7]
+
+
+def test_generator_is_seeded_and_shaped():
+    cfg = mo.baseline_configs()[0]
+    A1, W1, S1 = mo.make_config_inputs(cfg)
+    A2, W2, S2 = mo.make_config_inputs(cfg)
+    assert mo.sha256_of(A1, W1, S1) == mo.sha256_of(A2, W2, S2)
+    assert A1.shape == (16, 2048) and W1.shape == (2048, 1024) and S1.shape == (2048, 64)
+    assert S1.min() >= 122 and S1.max() <= 130
+    codes = mo.unpack_codes(W1, axis=1)
+    assert codes.min() == 0 and codes.max() == 15
+
+
+def test_tolerance_formula():
+    assert mo.atol_for(4096) == pytest.approx(1e-2)
+    assert mo.atol_for(16384) == pytest.approx(2e-2)
+    ref = np.array([1.0, 100.0])
+    assert mo.strict_violations(ref + np.array([0.029, 2.0]), ref, 4096) == 0
+    assert mo.strict_violations(ref + np.array([0.031, 0.0]), ref, 4096) == 1
