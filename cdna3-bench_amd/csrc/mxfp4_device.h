@@ -31,17 +31,19 @@ constexpr int kNumXcds = 8; // MI355X: 8 XCDs x 32 CUs
 constexpr uint32_t kOobOffset = 0x80000000u;
 constexpr uint32_t kNumRecords = 0x40000000u;
 
-// E8M0 byte -> fp32 by placing it in the exponent field: 2^(e-127) for
-// e = 1..254, +0.0 for e = 0, +inf for e = 255 (the GPU convention of the
-// reference, csrc/strategy_h_dequant.h:65-67).
+// E8M0 byte -> the scale operand of v_cvt_scalef32_pk_*: the byte goes in
+// the fp32 exponent field (as csrc/strategy_h_dequant.h:65-67 does).  The
+// convert reads only that field as an OCP MX E8M0 scale, so byte 0 scales by
+// 2^-127 (bf16 subnormals are kept: identical to ref.py:69) and byte 255 is
+// NaN (ref.py gives +-inf); measured on gfx950 by the exhaustive dequant test.
 __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
   return __builtin_bit_cast(float, (e & 0xFFu) << 23);
 }
 
 // Byte SEL of w holds two E2M1 codes (low nibble = even K).  Returns the two
-// bf16 values code * scale, element 0 (low half) from the low nibble.  One
-// v_cvt_scalef32_pk_bf16_fp4; exact, since every E2M1 value times a power of
-// two is a bf16 value in the normal range.
+// bf16 values code * 2^(e-127), element 0 (low half) from the low nibble.  One
+// v_cvt_scalef32_pk_bf16_fp4; exact for every scale byte 0..254 (an E2M1
+// value times a power of two fits bf16, subnormals included).
 template <int SEL>
 __device__ __forceinline__ uint32_t fp4x2_to_bf16x2(uint32_t w, float scale) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, SEL));
