@@ -27,23 +27,30 @@ struct TiledVariant {
   TiledShape shape;
   double eff;       // sustained fraction of the CU's MFMA peak
   int ctas_per_cu;  // residency (registers / LDS)
+  bool pipe;        // three-stage pipelined kernel (mxfp4_tiled_pipe.hip)
 };
 
 // Tile variants of the tiled family; index = mxfp4_plan.variant.
 const TiledVariant kTiled[] = {
-    {{2, 2, 4}, 0.70, 1},  // 0: 256 x 256, 4 waves, 128 x 128 per wave
-    {{4, 2, 2}, 0.70, 1},  // 1: 256 x 256, 8 waves
-    {{2, 2, 2}, 0.60, 2},  // 2: 128 x 256
-    {{1, 2, 2}, 0.45, 2},  // 3:  64 x 256
-    {{2, 1, 2}, 0.50, 2},  // 4: 128 x 128
-    {{1, 2, 1}, 0.30, 4},  // 5:  32 x 256
+    {{2, 2, 4}, 0.35, 1, false},  // 0: 256 x 256, 4 waves, 128 x 128 per wave
+    {{4, 2, 2}, 0.42, 1, false},  // 1: 256 x 256, 8 waves
+    {{2, 2, 2}, 0.30, 2, false},  // 2: 128 x 256
+    {{1, 2, 2}, 0.30, 2, false},  // 3:  64 x 256
+    {{2, 1, 2}, 0.25, 2, false},  // 4: 128 x 128
+    {{1, 2, 1}, 0.20, 4, false},  // 5:  32 x 256
+    {{4, 2, 2}, 0.60, 1, true},   // 6: 256 x 256, 8 waves, 3-stage pipeline
+    {{2, 2, 2}, 0.50, 1, true},   // 7: 128 x 256, 3-stage pipeline
+    {{2, 2, 4}, 0.50, 1, true},   // 8: 256 x 256, 4 waves, 3-stage pipeline
+    {{2, 1, 2}, 0.40, 1, true},   // 9: 128 x 128, 3-stage pipeline
 };
 constexpr int kNumTiled = sizeof(kTiled) / sizeof(kTiled[0]);
 
 // Shapes of the memory-bound family; index = mxfp4_plan.variant.
+// (mt, cb, wpc, u) -- same order as MXFP4_GEMV_SHAPES in mxfp4_gemv.hip.
 const GemvShape kGemv[] = {
-    {1, 16, 4}, {1, 8, 8}, {1, 8, 4}, {1, 4, 8}, {2, 8, 4},
-    {2, 4, 8},  {1, 2, 8}, {2, 2, 8}, {1, 2, 16}, {2, 2, 16},
+    {1, 8, 8, 4},  {1, 16, 8, 2}, {1, 8, 16, 2}, {1, 4, 16, 4}, {2, 8, 8, 2}, {2, 4, 16, 2},
+    {1, 2, 16, 4}, {2, 2, 16, 2}, {1, 4, 8, 4},  {1, 2, 8, 4},  {2, 4, 8, 2}, {1, 8, 4, 4},
+    {1, 2, 16, 2}, {1, 4, 16, 2}, {1, 8, 8, 2},
 };
 constexpr int kNumGemv = sizeof(kGemv) / sizeof(kGemv[0]);
 
@@ -66,24 +73,22 @@ bool gemv_plan_ok(int layout, int64_t M, int64_t N, const GemvShape& g) {
   return gemv_shape_available(layout, g);
 }
 
-// Memory-bound family: pick the shape and split count that keep enough bytes
-// in flight (>= 2 CTAs of 8+ waves per CU) with at least two K steps per wave.
+// Memory-bound family.  [N,K/2]: 32 columns x the whole K per CTA of 16
+// waves (no split needed once N >= 8192).  [K/2,N]: 128 columns per CTA and
+// K split so the grid has ~256 CTAs; the split partials cost 8*S*M/K of the
+// weight bytes, so S stays small.
 void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
-  const int mt = M <= 16 ? 1 : 2;
-  int want = -1;
-  for (int i = 0; i < kNumGemv; ++i) {
-    const GemvShape& g = kGemv[i];
-    if (g.mt != mt) continue;
-    if (layout == kLayoutKN && g.cb == 8 && g.wpc == (mt == 1 ? 8 : 4)) want = i;
-    if (layout == kLayoutNK && g.cb == 2 && g.wpc == 16) want = i;
-  }
+  const bool two = M > 16;
+  int want;
+  if (layout == kLayoutKN)
+    want = two ? 4 : 0;  // (2,8,8,2) / (1,8,8,4)
+  else
+    want = two ? 7 : 6;  // (2,2,16,2) / (1,2,16,4)
   const GemvShape& g = kGemv[want];
-  const int64_t cols = 16 * g.cb;
-  const int64_t groups = ceil_div(N, cols);
+  const int64_t groups = ceil_div(N, 16 * g.cb);
   const int64_t steps = gemv_steps(layout, K);
-  const int64_t target = layout == kLayoutKN ? 512 : 256;
-  int64_t splits = std::max<int64_t>(1, ceil_div(target, groups));
-  splits = std::min<int64_t>(splits, std::max<int64_t>(1, steps / (2 * g.wpc)));
+  int64_t splits = std::max<int64_t>(1, (256 + groups / 2) / groups);
+  splits = std::min<int64_t>(splits, std::max<int64_t>(1, steps / g.wpc));
   out->kernel = MXFP4_KERNEL_GEMV;
   out->variant = want;
   out->split_k = (int32_t)splits;
@@ -263,7 +268,8 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
       a.splits = (int)ceil_div(a.ksteps, a.steps_per_split);
       a.partials = a.splits > 1 ? partials : nullptr;
       a.counters = a.splits > 1 ? counters : nullptr;
-      return launch_tiled(layout, s, a, stream);
+      return kTiled[plan.variant].pipe ? launch_tiled_pipe(layout, s, a, stream)
+                                       : launch_tiled(layout, s, a, stream);
     }
     default:
       return hipErrorInvalidValue;
@@ -292,14 +298,15 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
       return hipSuccess;
     case MXFP4_KERNEL_GEMV:
       if (plan->variant < 0 || plan->variant >= kNumGemv) return hipErrorInvalidValue;
-      snprintf(buf, buf_len, "gemv mt%d cb%d wpc%d split%d", kGemv[plan->variant].mt,
-               kGemv[plan->variant].cb, kGemv[plan->variant].wpc, plan->split_k);
+      snprintf(buf, buf_len, "gemv mt%d cb%d wpc%d u%d split%d", kGemv[plan->variant].mt,
+               kGemv[plan->variant].cb, kGemv[plan->variant].wpc, kGemv[plan->variant].u,
+               plan->split_k);
       return hipSuccess;
     case MXFP4_KERNEL_TILED: {
       if (plan->variant < 0 || plan->variant >= kNumTiled) return hipErrorInvalidValue;
       const TiledShape& s = kTiled[plan->variant].shape;
-      snprintf(buf, buf_len, "tiled %dx%d w%dx%d split%d", s.bm(), s.bn(), s.wm, s.wn,
-               plan->split_k);
+      snprintf(buf, buf_len, "tiled%s %dx%d w%dx%d split%d", kTiled[plan->variant].pipe ? "-pipe" : "",
+               s.bm(), s.bn(), s.wm, s.wn, plan->split_k);
       return hipSuccess;
     }
     default:

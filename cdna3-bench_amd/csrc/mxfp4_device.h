@@ -95,6 +95,43 @@ __device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, v
 
 __device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Split-K partials cross XCDs, whose L2s are not coherent with each other.
+// Instead of __threadfence() (buffer_wbl2 + buffer_inv of the whole L2 on
+// gfx950, which flushes every CTA's cached tiles), the partials themselves
+// are written and read with SC1 (device-scope coherent) buffer accesses, the
+// same cache policy LLVM gives agent-scope atomic loads/stores.  A writer
+// waits for its SC1 stores (vmcnt) before the counter increment.
+constexpr int kCPolDevice = 16;  // SC1
+
+__device__ __forceinline__ void store_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCPolDevice);
+}
+__device__ __forceinline__ void store_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, kCPolDevice);
+}
+__device__ __forceinline__ f32x4 load_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCPolDevice));
+}
+__device__ __forceinline__ float load_coherent1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCPolDevice));
+}
+
+// Split-K arrival: every thread's SC1 partial stores have completed when
+// thread 0 bumps the tile counter; returns true in the CTA that arrived last
+// (it then owns the reduction and resets the counter for the next call).
+__device__ __forceinline__ bool splitk_arrive_last(uint32_t* counter, uint32_t splits, int* s_flag) {
+  wait_vmcnt0();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == splits - 1;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = last;
+  }
+  __syncthreads();
+  return *s_flag != 0;
+}
+
 // Workgroups are dispatched round-robin over the XCDs (id % 8).  Renumber so
 // each XCD owns one contiguous range of logical ids; a bijection for any
 // count.  Neighbouring logical tiles then share an XCD's L2.

@@ -28,12 +28,16 @@
 namespace mxfp4 {
 namespace {
 
-template <int LAYOUT, int MT, int CB, int WPC>
+template <int LAYOUT, int MT, int CB, int WPC, int U>
 struct GemvCfg {
   static constexpr int NT = WPC * 64;
   static constexpr int COLS = 16 * CB;
   static constexpr int ROWS = 16 * MT;
   static constexpr int TILE = ROWS * COLS;  // floats per CTA partial
+  // The wave reduction runs over column chunks so its LDS stays <= 64 KB.
+  static constexpr int CHUNKS = (WPC * TILE * 4 + 65535) / 65536;
+  static constexpr int CCOLS = COLS / CHUNKS;
+  static constexpr int CTILE = ROWS * CCOLS;
 };
 
 template <int LAYOUT, int MT, int CB>
@@ -66,14 +70,16 @@ __device__ __forceinline__ void load_words(uint32_t (&dst)[N_], const uint8_t* s
   }
 }
 
-template <int LAYOUT, int MT, int CB, int WPC>
+template <int LAYOUT, int MT, int CB, int WPC, int U>
 __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
-  using Cfg = GemvCfg<LAYOUT, MT, CB, WPC>;
+  using Cfg = GemvCfg<LAYOUT, MT, CB, WPC, U>;
   constexpr int NT = Cfg::NT, COLS = Cfg::COLS, TILE = Cfg::TILE;
-  __shared__ __attribute__((aligned(16))) float red[WPC * TILE];
+  constexpr int CHUNKS = Cfg::CHUNKS, CCOLS = Cfg::CCOLS, CTILE = Cfg::CTILE;
+  __shared__ __attribute__((aligned(16))) float red[WPC * CTILE];
   __shared__ int s_last;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int c = lane & 15, q = lane >> 4;
   const int M = p.M, N = p.N, K = p.K;
   const int Kh = K >> 1, G = K >> 5;
@@ -85,6 +91,10 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
   const int n0 = cg * COLS;
   const int s_begin = split * p.steps_per_split;
   const int s_end = min(p.steps, s_begin + p.steps_per_split);
+  // Each wave owns a contiguous run of the CTA's K steps.
+  const int per_wave = (s_end - s_begin + WPC - 1) / WPC;
+  const int w_begin = s_begin + wave * per_wave;
+  const int w_end = min(s_end, w_begin + per_wave);
 
   f32x4 acc[MT][CB];
 #pragma unroll
@@ -94,10 +104,10 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
 
   using Regs = GemvRegs<LAYOUT, MT, CB>;
 
-  auto load = [&](Regs& r, int st) {
+  auto load = [&](Regs& r, int st, bool live) {
     if constexpr (LAYOUT == kLayoutKN) {
       const int col = n0 + c * CB;
-      const bool cok = col < N;
+      const bool cok = live && col < N;
       const uint8_t* bp = p.B + (size_t)(st * 16 + 4 * q) * N + col;
 #pragma unroll
       for (int i = 0; i < 4; ++i) load_words(r.raw[i], bp + (size_t)i * N, cok);
@@ -105,12 +115,12 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = mt * 16 + c;
-        r.a[mt] = (m < M) ? *reinterpret_cast<const u32x4*>(p.A + (size_t)m * K + st * 32 + 8 * q)
-                          : u32x4{0u, 0u, 0u, 0u};
+        r.a[mt] = (live && m < M) ? *reinterpret_cast<const u32x4*>(p.A + (size_t)m * K + st * 32 + 8 * q)
+                                  : u32x4{0u, 0u, 0u, 0u};
       }
     } else {
       const int k0 = st * 128 + 32 * q;  // this lane's K group
-      const bool kok = k0 < K;
+      const bool kok = live && k0 < K;
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
         const int col = n0 + cb * 16 + c;
@@ -162,113 +172,120 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
     }
   };
 
-  // Waves interleave over the CTA's steps; one step of loads in flight ahead.
-  int st = s_begin + wave;
-  if (st < s_end) {
-    Regs cur;
-    load(cur, st);
-    for (; st < s_end; st += WPC) {
-      Regs nxt;
-      const bool more = st + WPC < s_end;
-      if (more) load(nxt, st + WPC);
-      compute(cur);
-      if (more) cur = nxt;
-    }
+  // U steps of loads in flight before any compute.
+  for (int st = w_begin; st < w_end; st += U) {
+    Regs r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) load(r[u], st + u, st + u < w_end);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (st + u < w_end) compute(r[u]);
   }
 
-  // ---- CTA reduction over waves (LDS, wave order) ---------------------------
-  float* my = red + wave * TILE;
+  // ---- CTA reduction over waves (LDS, wave order), CHUNKS column chunks ----
+  constexpr int PER = (CTILE + NT - 1) / NT;  // elements per thread per chunk
+  float v[CHUNKS][PER];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int ch = 0; ch < CHUNKS; ++ch) {
+    float* my = red + wave * CTILE;
 #pragma unroll
-    for (int j = 0; j < CB; ++j)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = mt * 16 + 4 * q + i;
+      for (int j = 0; j < CB; ++j) {
         const int col = (LAYOUT == kLayoutKN) ? c * CB + j : j * 16 + c;
-        my[row * COLS + col] = acc[mt][j][i];
+        if (col / CCOLS != ch) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) my[(mt * 16 + 4 * q + i) * CCOLS + col % CCOLS] = acc[mt][j][i];
       }
-  __syncthreads();
-
-  constexpr int PER = (TILE + NT - 1) / NT;  // elements per thread
-  float v[PER];
+    __syncthreads();
 #pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int idx = e * NT + threadIdx.x;
-    if (TILE % NT != 0 && idx >= TILE) { v[e] = 0.f; continue; }
-    float s = red[idx];
+    for (int e = 0; e < PER; ++e) {
+      const int idx = e * NT + threadIdx.x;
+      float sum = 0.f;
+      if (CTILE % NT == 0 || idx < CTILE) {
+        sum = red[idx];
 #pragma unroll
-    for (int w = 1; w < WPC; ++w) s += red[w * TILE + idx];
-    v[e] = s;
+        for (int w = 1; w < WPC; ++w) sum += red[w * CTILE + idx];
+      }
+      v[ch][e] = sum;
+    }
+    __syncthreads();
   }
+
+  // element (ch, e) <-> tile row / column
+  auto row_of = [&](int e) { return (e * NT + (int)threadIdx.x) / CCOLS; };
+  auto col_of = [&](int ch, int e) { return ch * CCOLS + (e * NT + (int)threadIdx.x) % CCOLS; };
+  auto live = [&](int e) { return (CTILE % NT == 0 || e * NT + (int)threadIdx.x < CTILE); };
 
   if (p.splits > 1) {
-    float* slot = p.partials + ((size_t)cg * p.splits + split) * TILE;
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(p.partials + (size_t)cg * p.splits * TILE);
 #pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const int idx = e * NT + threadIdx.x;
-      if (idx < TILE && idx / COLS < M) slot[idx] = v[e];
-    }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t prev = atomicAdd(p.counters + cg, 1u);
-      s_last = (prev == (uint32_t)(p.splits - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const float* base = p.partials + (size_t)cg * p.splits * TILE;
+    for (int ch = 0; ch < CHUNKS; ++ch)
 #pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const int idx = e * NT + threadIdx.x;
-      if (idx >= TILE || idx / COLS >= M) continue;
-      float s = base[idx];
-      for (int sp = 1; sp < p.splits; ++sp) s += base[(size_t)sp * TILE + idx];
-      v[e] = s;
-    }
-    if (threadIdx.x == 0) p.counters[cg] = 0u;
+      for (int e = 0; e < PER; ++e)
+        if (live(e) && row_of(e) < M)
+          store_coherent(rp, (uint32_t)((split * TILE + row_of(e) * COLS + col_of(ch, e)) * 4), v[ch][e]);
+    if (!splitk_arrive_last(p.counters + cg, (uint32_t)p.splits, &s_last)) return;
+#pragma unroll
+    for (int ch = 0; ch < CHUNKS; ++ch)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        if (!live(e) || row_of(e) >= M) continue;
+        const uint32_t off = (uint32_t)((row_of(e) * COLS + col_of(ch, e)) * 4);
+        float sum = load_coherent1(rp, off);
+        for (int sp = 1; sp < p.splits; ++sp) sum += load_coherent1(rp, off + (uint32_t)(sp * TILE * 4));
+        v[ch][e] = sum;
+      }
   }
 
 #pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int idx = e * NT + threadIdx.x;
-    const int row = idx / COLS, col = n0 + idx % COLS;
-    if (idx < TILE && row < M && col < N) {
-      if (p.out_bf16)
-        static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(v[e]);
-      else
-        static_cast<float*>(p.C)[(size_t)row * N + col] = v[e];
+  for (int ch = 0; ch < CHUNKS; ++ch)
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int row = row_of(e), col = n0 + col_of(ch, e);
+      if (live(e) && row < M && col < N) {
+        if (p.out_bf16)
+          static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(v[ch][e]);
+        else
+          static_cast<float*>(p.C)[(size_t)row * N + col] = v[ch][e];
+      }
     }
-  }
 }
 
-template <int LAYOUT, int MT, int CB, int WPC>
+template <int LAYOUT, int MT, int CB, int WPC, int U>
 hipError_t launch_one(const GemvArgs& a, hipStream_t stream) {
-  using Cfg = GemvCfg<LAYOUT, MT, CB, WPC>;
+  using Cfg = GemvCfg<LAYOUT, MT, CB, WPC, U>;
+  static_assert(Cfg::COLS % Cfg::CHUNKS == 0, "column chunks must divide the tile");
   const int grid = a.col_groups * a.splits;
-  hipLaunchKernelGGL((gemv_kernel<LAYOUT, MT, CB, WPC>), dim3(grid), dim3(Cfg::NT), 0, stream, a);
+  hipLaunchKernelGGL((gemv_kernel<LAYOUT, MT, CB, WPC, U>), dim3(grid), dim3(Cfg::NT), 0, stream, a);
   return hipGetLastError();
 }
 
+// (MT, CB, WPC, U); index = plan variant.  [K/2,N] needs CB >= 4.
 #define MXFP4_GEMV_SHAPES(X) \
-  X(1, 16, 4)                \
-  X(1, 8, 8)                 \
-  X(1, 8, 4)                 \
-  X(1, 4, 8)                 \
-  X(2, 8, 4)                 \
-  X(2, 4, 8)                 \
-  X(1, 2, 8)                 \
-  X(2, 2, 8)                 \
-  X(1, 2, 16)                \
-  X(2, 2, 16)
+  X(1, 8, 8, 4)              \
+  X(1, 16, 8, 2)             \
+  X(1, 8, 16, 2)             \
+  X(1, 4, 16, 4)             \
+  X(2, 8, 8, 2)              \
+  X(2, 4, 16, 2)             \
+  X(1, 2, 16, 4)             \
+  X(2, 2, 16, 2)             \
+  X(1, 4, 8, 4)              \
+  X(1, 2, 8, 4)              \
+  X(2, 4, 8, 2)              \
+  X(1, 8, 4, 4)              \
+  X(1, 2, 16, 2)             \
+  X(1, 4, 16, 2)             \
+  X(1, 8, 8, 2)
 
 template <int LAYOUT>
 hipError_t dispatch(const GemvShape& s, const GemvArgs& a, hipStream_t stream) {
-#define X(MT_, CB_, WPC_)                                    \
-  if constexpr (LAYOUT == kLayoutNK || CB_ >= 4) {           \
-    if (s.mt == MT_ && s.cb == CB_ && s.wpc == WPC_)         \
-      return launch_one<LAYOUT, MT_, CB_, WPC_>(a, stream);  \
+#define X(MT_, CB_, WPC_, U_)                                   \
+  if constexpr (LAYOUT == kLayoutNK || CB_ >= 4) {              \
+    if (s.mt == MT_ && s.cb == CB_ && s.wpc == WPC_ && s.u == U_) \
+      return launch_one<LAYOUT, MT_, CB_, WPC_, U_>(a, stream); \
   }
   MXFP4_GEMV_SHAPES(X)
 #undef X
@@ -279,8 +296,8 @@ hipError_t dispatch(const GemvShape& s, const GemvArgs& a, hipStream_t stream) {
 
 bool gemv_shape_available(int layout, const GemvShape& s) {
   if (layout == kLayoutKN && s.cb == 2) return false;  // [K/2,N] needs >= 4 bytes per lane row
-#define X(MT_, CB_, WPC_) \
-  if (s.mt == MT_ && s.cb == CB_ && s.wpc == WPC_) return true;
+#define X(MT_, CB_, WPC_, U_) \
+  if (s.mt == MT_ && s.cb == CB_ && s.wpc == WPC_ && s.u == U_) return true;
   MXFP4_GEMV_SHAPES(X)
 #undef X
   return false;

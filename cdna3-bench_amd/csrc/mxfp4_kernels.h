@@ -54,13 +54,19 @@ struct GemvArgs {
 struct GemvShape {
   int mt;    // 16-row MFMA tiles (1: M <= 16, 2: M <= 32)
   int cb;    // [K/2,N]: bytes per lane per K-pair row (4, 8, 16); [N,K/2]: 16-column blocks per wave
-  int wpc;   // waves per CTA (all on the same columns, K interleaved)
-  int cols(int layout) const { return layout == kLayoutKN ? 16 * cb : 16 * cb; }
+  int wpc;   // waves per CTA (all on the same columns, each a run of K steps)
+  int u;     // K steps of loads issued before compute
+  int cols() const { return 16 * cb; }
 };
 
 hipError_t launch_tiled(int layout, const TiledShape& shape, const TiledArgs& args,
                         hipStream_t stream);
 bool tiled_shape_available(int layout, const TiledShape& shape);
+
+// Three-stage pipelined variant of the tiled family (mxfp4_tiled_pipe.hip).
+hipError_t launch_tiled_pipe(int layout, const TiledShape& shape, const TiledArgs& args,
+                             hipStream_t stream);
+bool tiled_pipe_shape_available(int layout, const TiledShape& shape);
 
 hipError_t launch_gemv(int layout, const GemvShape& shape, const GemvArgs& args,
                        hipStream_t stream);

@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_kernel(TiledArgs p) {
   __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int wm = wave / WN, wn = wave % WN;
   const int c = lane & 31, h = lane >> 5;
 
@@ -246,42 +246,38 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_kernel(TiledArgs p) {
   }
 
   // ---- split-K fix-up ------------------------------------------------------
+  // Partial slot of (tile, split): [quad][thread] f32x4, written and read with
+  // device-coherent (SC1) accesses; the last CTA of the tile sums the splits
+  // in split order (deterministic).
   if (p.splits > 1) {
     constexpr int Q = RB * 16;  // f32x4 quads per thread
-    f32x4* slot = reinterpret_cast<f32x4*>(p.partials) + ((size_t)tile * p.splits + split) * (Q * NT);
+    constexpr uint32_t SLOT = (uint32_t)Q * NT * 16;  // bytes per split slot
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(reinterpret_cast<uint8_t*>(p.partials) + (size_t)tile * p.splits * SLOT);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-          f32x4 v = {acc[rb][j][q4 * 4 + 0], acc[rb][j][q4 * 4 + 1], acc[rb][j][q4 * 4 + 2],
-                     acc[rb][j][q4 * 4 + 3]};
-          slot[((rb * 4 + j) * 4 + q4) * NT + threadIdx.x] = v;
+          const f32x4 v = {acc[rb][j][q4 * 4 + 0], acc[rb][j][q4 * 4 + 1], acc[rb][j][q4 * 4 + 2],
+                           acc[rb][j][q4 * 4 + 3]};
+          const uint32_t off = split * SLOT + (uint32_t)(((rb * 4 + j) * 4 + q4) * NT + threadIdx.x) * 16;
+          store_coherent(rp, off, v);
         }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t prev = atomicAdd(p.counters + tile, 1u);
-      s_last = (prev == (uint32_t)(p.splits - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const f32x4* base = reinterpret_cast<const f32x4*>(p.partials) + (size_t)tile * p.splits * (Q * NT);
+    if (!splitk_arrive_last(p.counters + tile, (uint32_t)p.splits, &s_last)) return;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-          const size_t idx = (size_t)((rb * 4 + j) * 4 + q4) * NT + threadIdx.x;
-          f32x4 sum = base[idx];
-          for (int sp = 1; sp < p.splits; ++sp) sum += base[(size_t)sp * (Q * NT) + idx];
+          const uint32_t off = (uint32_t)(((rb * 4 + j) * 4 + q4) * NT + threadIdx.x) * 16;
+          f32x4 sum = load_coherent4(rp, off);
+          for (int sp = 1; sp < p.splits; ++sp) sum += load_coherent4(rp, sp * SLOT + off);
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[rb][j][q4 * 4 + e] = sum[e];
         }
-    if (threadIdx.x == 0) p.counters[tile] = 0u;
   }
 
   // ---- epilogue ------------------------------------------------------------

@@ -121,8 +121,8 @@ def test_generic_kernel_odd_n(kk):
         assert mo.strict_violations(out, ref, K) == 0
 
 
-TILED_VARIANTS = range(6)
-GEMV_VARIANTS = range(10)
+TILED_VARIANTS = range(10)
+GEMV_VARIANTS = range(15)
 
 
 @pytest.mark.parametrize("layout", ["kn", "nk"])
