@@ -32,16 +32,21 @@ struct TiledVariant {
 
 // Tile variants of the tiled family; index = mxfp4_plan.variant.
 const TiledVariant kTiled[] = {
-    {{2, 2, 4}, 0.35, 1, false},  // 0: 256 x 256, 4 waves, 128 x 128 per wave
-    {{4, 2, 2}, 0.42, 1, false},  // 1: 256 x 256, 8 waves
-    {{2, 2, 2}, 0.30, 2, false},  // 2: 128 x 256
-    {{1, 2, 2}, 0.30, 2, false},  // 3:  64 x 256
-    {{2, 1, 2}, 0.25, 2, false},  // 4: 128 x 128
-    {{1, 2, 1}, 0.20, 4, false},  // 5:  32 x 256
-    {{4, 2, 2}, 0.60, 1, true},   // 6: 256 x 256, 8 waves, 3-stage pipeline
-    {{2, 2, 2}, 0.50, 1, true},   // 7: 128 x 256, 3-stage pipeline
-    {{2, 2, 4}, 0.50, 1, true},   // 8: 256 x 256, 4 waves, 3-stage pipeline
-    {{2, 1, 2}, 0.40, 1, true},   // 9: 128 x 128, 3-stage pipeline
+    {{2, 2, 4}, 0.35, 1, false},        // 0: 256 x 256, 4 waves, 128 x 128 per wave
+    {{4, 2, 2}, 0.42, 1, false},        // 1: 256 x 256, 8 waves
+    {{2, 2, 2}, 0.30, 2, false},        // 2: 128 x 256
+    {{1, 2, 2}, 0.30, 2, false},        // 3:  64 x 256
+    {{2, 1, 2}, 0.25, 2, false},        // 4: 128 x 128
+    {{1, 2, 1}, 0.20, 4, false},        // 5:  32 x 256
+    {{4, 2, 2, 4, 3}, 0.48, 1, true},   // 6: pipelined 256 x 256, 8 waves of 64 x 128, 3 stages
+    {{2, 2, 2, 4, 3}, 0.40, 1, true},   // 7: pipelined 128 x 256, 4 waves of 64 x 128
+    {{4, 2, 2, 4, 4}, 0.54, 1, true},   // 8: as 6 with a 4-stage ring (160 KB)
+    {{2, 4, 4, 2, 4}, 0.56, 1, true},   // 9: pipelined 256 x 256, 8 waves of 128 x 64, 4 stages
+    {{2, 4, 4, 2, 3}, 0.50, 1, true},   // 10: as 9 with 3 stages
+    {{2, 2, 2, 4, 4}, 0.42, 1, true},   // 11: as 7 with 4 stages
+    {{2, 4, 2, 2, 4}, 0.42, 1, true},   // 12: pipelined 128 x 256, 8 waves of 64 x 64
+    {{1, 4, 4, 2, 4}, 0.44, 1, true},   // 13: pipelined 128 x 256, 4 waves of 128 x 64
+    {{2, 1, 2, 4, 4}, 0.36, 2, true},   // 14: pipelined 128 x 128, 2 waves
 };
 constexpr int kNumTiled = sizeof(kTiled) / sizeof(kTiled[0]);
 
@@ -305,8 +310,11 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
     case MXFP4_KERNEL_TILED: {
       if (plan->variant < 0 || plan->variant >= kNumTiled) return hipErrorInvalidValue;
       const TiledShape& s = kTiled[plan->variant].shape;
-      snprintf(buf, buf_len, "tiled%s %dx%d w%dx%d split%d", kTiled[plan->variant].pipe ? "-pipe" : "",
-               s.bm(), s.bn(), s.wm, s.wn, plan->split_k);
+      if (kTiled[plan->variant].pipe)
+        snprintf(buf, buf_len, "tiled-pipe %dx%d w%dx%d ns%d split%d", s.bm(), s.bn(), s.wm, s.wn,
+                 s.stages, plan->split_k);
+      else
+        snprintf(buf, buf_len, "tiled %dx%d w%dx%d split%d", s.bm(), s.bn(), s.wm, s.wn, plan->split_k);
       return hipSuccess;
     }
     default:

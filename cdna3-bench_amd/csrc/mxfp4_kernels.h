@@ -29,9 +29,11 @@ struct TiledArgs {
 };
 
 struct TiledShape {
-  int wm, wn, rb;  // waves along M, waves along N, 32-row blocks per wave
+  int wm, wn, rb;   // waves along M, waves along N, 32-row blocks per wave
+  int wnc = 4;      // 32-column MFMA blocks per wave (pipelined kernel: 2 or 4)
+  int stages = 3;   // pipelined kernel: LDS ring depth
   int bm() const { return wm * rb * 32; }
-  int bn() const { return wn * 128; }
+  int bn() const { return wn * 32 * wnc; }
   int threads() const { return wm * wn * 64; }
 };
 

@@ -1,16 +1,28 @@
 // Pipelined tiled MFMA kernel (M > 32): the production kernel of the tiled
-// family.  Same tile geometry, operand layouts, loaders and split-K protocol
-// as tiled_kernel (mxfp4_tiled.hip); the main loop differs:
+// family.  Same operand layouts, loaders and split-K protocol as tiled_kernel
+// (mxfp4_tiled.hip); the main loop differs:
 //
-//   * three LDS stages in a ring: while stage t is consumed, stage t+1 is
-//     resident and stage t+2 is in flight (16-byte buffer_load ... lds);
+//   * an NS-stage LDS ring: while stage t is consumed, stages t+1 .. t+NS-1
+//     are resident or in flight (16-byte buffer_load ... lds);
 //   * LDS operands are read one 16-K sub-step ahead into registers, so the
 //     ds_read latency of sub-step s+1 hides under the MFMAs of sub-step s;
 //   * one barrier per stage, placed before the last sub-step: it publishes
 //     stage t+1 (every wave waited for its own loads with a counted vmcnt)
-//     and retires stage t-1's buffer, and the first operands of stage t+1
-//     are read while the last MFMAs of stage t drain -- no pipeline bubble at
-//     the stage boundary.
+//     and retires stage t-1's buffer; the first operands of stage t+1 are
+//     read while the last MFMAs of stage t drain;
+//   * the per-lane LDS offsets (XOR swizzles included) are computed once; a
+//     sub-step read is one add of the stage base plus immediate offsets.
+//
+// Wave tile: RB 32-row blocks x (32 * WNC) columns.  Every B element is
+// converted once per wave that reads it, i.e. (BM / wave rows) times per
+// tile: converts per MFMA = 128 / (32 * RB).  WNC = 4 with RB = 2 (4 x 2
+// waves of 64 x 128) or WNC = 2 with RB = 4 (2 x 4 waves of 128 x 64).
+//   [K/2,N] weights: a lane reads WNC bytes (WNC adjacent columns) of each of
+//     4 K-pair rows; MFMA j uses byte j of each row word (WNC = 4) or bytes j,
+//     j+2 of two packed row pairs (WNC = 2), so MFMA j covers columns
+//     WNC*c + j and the epilogue writes WNC adjacent columns per lane.
+//   [N,K/2] weights: a lane reads 16 bytes = 32 K of column block cb; word s
+//     against the A chunk K 32h + 8s .. +7.
 //
 // Reference counterpart: the K loop of strategy_j/strategy_m
 // (csrc/strategy_j_synthesis.cu:120-170, csrc/strategy_m_asm.cu:131-185),
@@ -22,12 +34,8 @@ namespace mxfp4 {
 namespace {
 
 constexpr int kBK = 64;
-constexpr int kStages = 3;
 
 __device__ __forceinline__ int a_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
-template <int CPR>
-__device__ __forceinline__ int kn_swz(int row) { return ((row >> 2) & 1) * (CPR / 2); }
-__device__ __forceinline__ int nk_swz(int row) { return (row >> 2) & 1; }
 
 // s_waitcnt vmcnt(N) with expcnt/lgkmcnt left at their maxima (gfx9 encoding).
 template <int N>
@@ -36,12 +44,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int LAYOUT, int WM, int WN, int RB>
+template <int LAYOUT, int WM, int WN, int RB, int WNC>
 struct PipeCfg {
   static constexpr int NWAVES = WM * WN;
   static constexpr int NT = NWAVES * 64;
   static constexpr int BM = WM * RB * 32;
-  static constexpr int BN = WN * 128;
+  static constexpr int WCOLS = 32 * WNC;  // columns per wave
+  static constexpr int BN = WN * WCOLS;
   static constexpr int A_BYTES = BM * 128;
   static constexpr int B_BYTES = BN * 32;
   static constexpr int STAGE = A_BYTES + B_BYTES;
@@ -50,32 +59,34 @@ struct PipeCfg {
   static_assert(A_INSTR % NWAVES == 0 && B_INSTR % NWAVES == 0, "loads split evenly over waves");
   static constexpr int A_PER_WAVE = A_INSTR / NWAVES;
   static constexpr int B_PER_WAVE = B_INSTR / NWAVES;
-  static constexpr int SC_LOADS = LAYOUT == kLayoutKN ? 2 : 4;
-  // VMEM instructions one wave issues per iteration (next-next stage + next scales).
+  static constexpr int SC_LOADS = LAYOUT == kLayoutKN ? 2 : WNC;
+  // VMEM instructions one wave issues per iteration (one stage + next scales).
   static constexpr int VM_PER_ITER = A_PER_WAVE + B_PER_WAVE + SC_LOADS;
-  static constexpr int KN_CPR = BN / 16;
+  static constexpr int KN_CPR = BN / 16;  // 16-byte chunks per K-pair row
 };
 
-template <int LAYOUT, int RB>
+template <int LAYOUT, int RB, int WNC>
 struct SubOps;  // operands of one 16-K sub-step
 
-template <int RB>
-struct SubOps<kLayoutKN, RB> {
+template <int RB, int WNC>
+struct SubOps<kLayoutKN, RB, WNC> {
   bf16x8 a[RB];
-  uint32_t raw[4];
+  uint32_t raw[WNC == 4 ? 4 : 2];  // WNC=4: row words; WNC=2: packed row pairs (0,1), (2,3)
 };
 
-template <int RB>
-struct SubOps<kLayoutNK, RB> {
+template <int RB, int WNC>
+struct SubOps<kLayoutNK, RB, WNC> {
   bf16x8 a[RB];
 };
 
-template <int LAYOUT, int WM, int WN, int RB>
+template <int LAYOUT, int WM, int WN, int RB, int WNC, int NS>
 __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p) {
-  using Cfg = PipeCfg<LAYOUT, WM, WN, RB>;
-  constexpr int NT = Cfg::NT, BM = Cfg::BM, BN = Cfg::BN;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * Cfg::STAGE];
-  __shared__ int s_last;
+  using Cfg = PipeCfg<LAYOUT, WM, WN, RB, WNC>;
+  constexpr int NT = Cfg::NT, BM = Cfg::BM, BN = Cfg::BN, WCOLS = Cfg::WCOLS;
+  static_assert(NS >= 3, "the barrier placement needs at least three stages");
+  static_assert(WNC == 2 || WNC == 4, "wave column width");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * Cfg::STAGE];
+  int* s_last = reinterpret_cast<int*>(smem);  // split-K flag; the ring is dead by then
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
@@ -122,7 +133,8 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
         const int i = wave * Cfg::B_PER_WAVE + ii;
         const int q = i * 64 + lane;
         const int row = q / CPR;
-        const int lc = (q % CPR) ^ kn_swz<CPR>(row);
+        // rows with bit 2 set store their two row halves swapped
+        const int lc = (q % CPR) ^ (((row >> 2) & 1) * (CPR / 2));
         const bool ok = ((k0 >> 1) + row < Kh) && (n0 + lc * 16 < N);
         buffer_load_lds16(rb, sB + i * 1024, ok ? (uint32_t)(row * N + lc * 16) : kOobOffset);
       }
@@ -133,97 +145,136 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
         const int i = wave * Cfg::B_PER_WAVE + ii;
         const int q = i * 64 + lane;
         const int row = q >> 1;
-        const int lc = (q & 1) ^ nk_swz(row);
+        const int lc = (q & 1) ^ ((row >> 2) & 1);  // rows with bit 2 set swap their chunks
         const bool ok = (n0 + row < N) && ((k0 >> 1) + lc * 16 < Kh);
         buffer_load_lds16(rb, sB + i * 1024, ok ? (uint32_t)(row * Kh + lc * 16) : kOobOffset);
       }
     }
   };
 
-  // Scales straight from global (L2-resident) one stage ahead.  Exactly
-  // SC_LOADS VMEM instructions per call (masked lanes load nothing).
+  // Scales straight from global (L2-resident) one stage ahead; exactly
+  // SC_LOADS VMEM instructions per call (masked lanes fetch nothing).
   auto load_scales = [&](uint32_t (&dst)[4], int step) {
     const int g0 = step * 2;
     if constexpr (LAYOUT == kLayoutKN) {
-      const int col = n0 + wn * 128 + 4 * c;
-      const bool cok = col < N;
-      const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.S + (size_t)g0 * N + n0 + wn * 128);
+      const bool cok = n0 + wn * WCOLS + WNC * c < N;
+      const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.S + (size_t)g0 * N + n0 + wn * WCOLS);
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
-        const bool ok = cok && (g0 + g < G);
-        dst[g] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)(g * N + 4 * c) : kOobOffset, 0, 0);
+        const uint32_t off = (cok && g0 + g < G) ? (uint32_t)(g * N + WNC * c) : kOobOffset;
+        if constexpr (WNC == 4)
+          dst[g] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+        else
+          dst[g] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
       }
     } else {
-      const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.S + (size_t)(n0 + wn * 128) * G + g0);
+      const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.S + (size_t)(n0 + wn * WCOLS) * G + g0);
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
-        const int col = n0 + wn * 128 + 32 * cb + c;
-        const bool ok = (g0 + h < G) && (col < N);
-        dst[cb] = __builtin_amdgcn_raw_buffer_load_b8(
-            rs, ok ? (uint32_t)((32 * cb + c) * G + h) : kOobOffset, 0, 0);
+      for (int cb = 0; cb < WNC; ++cb) {
+        const bool ok = (g0 + h < G) && (n0 + wn * WCOLS + 32 * cb + c < N);
+        dst[cb] = __builtin_amdgcn_raw_buffer_load_b8(rs, ok ? (uint32_t)((32 * cb + c) * G + h) : kOobOffset, 0, 0);
       }
     }
   };
+
+  // ---- per-lane LDS offsets (loop invariant) ---------------------------------
+  // A: row wm*RB*32 + 32*rb + c; its swizzle ignores rb (bit 5).
+  uint32_t a_off[4];
+  {
+    const int row = wm * RB * 32 + c;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int lc = LAYOUT == kLayoutKN ? ks * 2 + h : h * 4 + ks;
+      a_off[ks] = (uint32_t)(row * 128 + ((lc ^ a_swz(row)) * 16));
+    }
+  }
+  // B: [K/2,N] row ks*8 + 4h + i (its swizzle depends on h only);
+  //    [N,K/2] row wn*WCOLS + 32*cb + c (its swizzle depends on c only).
+  uint32_t b_off;
+  if constexpr (LAYOUT == kLayoutKN) {
+    constexpr int CPR = Cfg::KN_CPR;
+    const int byte = wn * WCOLS + WNC * c;
+    b_off = (uint32_t)(Cfg::A_BYTES + h * 4 * BN + (((byte >> 4) ^ (h * (CPR / 2))) * 16) + (byte & 15));
+  } else {
+    b_off = (uint32_t)(Cfg::A_BYTES + (wn * WCOLS + c) * 32 + ((h ^ ((c >> 2) & 1)) * 16));
+  }
 
   // ---- LDS -> registers ------------------------------------------------------
-  using Ops = SubOps<LAYOUT, RB>;
+  using Ops = SubOps<LAYOUT, RB, WNC>;
   auto read_ops = [&](int buf, int ks, Ops& o) {
-    const uint8_t* sA = smem + buf * Cfg::STAGE;
-    const uint8_t* sB = sA + Cfg::A_BYTES;
+    const uint8_t* base = smem + buf * Cfg::STAGE;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int row = wm * RB * 32 + rb * 32 + c;
-      const int lc = LAYOUT == kLayoutKN ? ks * 2 + h : h * 4 + ks;
-      o.a[rb] = *reinterpret_cast<const bf16x8*>(sA + row * 128 + ((lc ^ a_swz(row)) * 16));
-    }
+    for (int rb = 0; rb < RB; ++rb)
+      o.a[rb] = *reinterpret_cast<const bf16x8*>(base + a_off[ks] + rb * 32 * 128);
     if constexpr (LAYOUT == kLayoutKN) {
-      constexpr int CPR = Cfg::KN_CPR;
+      const uint8_t* pb = base + b_off + ks * 8 * BN;
+      if constexpr (WNC == 4) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = ks * 8 + h * 4 + i;
-        const int lc = (wn * 128 + 4 * c) >> 4;
-        o.raw[i] = *reinterpret_cast<const uint32_t*>(sB + row * BN + (lc ^ kn_swz<CPR>(row)) * 16 + 4 * (c & 3));
+        for (int i = 0; i < 4; ++i) o.raw[i] = *reinterpret_cast<const uint32_t*>(pb + i * BN);
+      } else {
+        const uint32_t r0 = *reinterpret_cast<const uint16_t*>(pb);
+        const uint32_t r1 = *reinterpret_cast<const uint16_t*>(pb + BN);
+        const uint32_t r2 = *reinterpret_cast<const uint16_t*>(pb + 2 * BN);
+        const uint32_t r3 = *reinterpret_cast<const uint16_t*>(pb + 3 * BN);
+        o.raw[0] = r0 | (r1 << 16);
+        o.raw[1] = r2 | (r3 << 16);
       }
     }
   };
-  // [N,K/2]: the 4 column blocks' 16 bytes for the whole stage.
-  auto read_braw = [&](int buf, u32x4 (&raw)[4]) {
-    const uint8_t* sB = smem + buf * Cfg::STAGE + Cfg::A_BYTES;
+  // [N,K/2]: the column blocks' 16 bytes for the whole stage.
+  auto read_braw = [&](int buf, u32x4 (&raw)[WNC]) {
+    const uint8_t* base = smem + buf * Cfg::STAGE + b_off;
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const int row = wn * 128 + cb * 32 + c;
-      raw[cb] = *reinterpret_cast<const u32x4*>(sB + row * 32 + ((h ^ nk_swz(row)) * 16));
-    }
+    for (int cb = 0; cb < WNC; ++cb) raw[cb] = *reinterpret_cast<const u32x4*>(base + cb * 32 * 32);
   };
 
-  f32x16 acc[RB][4];
+  f32x16 acc[RB][WNC];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < WNC; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[rb][j][e] = 0.f;
 
-  // cvt + MFMA for one sub-step.
-  auto mma_kn = [&](const SubOps<kLayoutKN, RB>& o, uint32_t sw) {
-    const float s0 = e8m0_to_f32(sw), s1 = e8m0_to_f32(sw >> 8);
-    const float s2 = e8m0_to_f32(sw >> 16), s3 = e8m0_to_f32(sw >> 24);
-    const bf16x8 b0 = operand_from_bytes<0>(o.raw[0], o.raw[1], o.raw[2], o.raw[3], s0);
+  // cvt + MFMA for one sub-step; sc = the column scales of its K group.
+  auto mma_kn = [&](const Ops& o, const float (&sc)[WNC]) {
+    if constexpr (LAYOUT != kLayoutKN) {
+      (void)o;
+      (void)sc;
+    } else if constexpr (WNC == 4) {
+      const bf16x8 b0 = operand_from_bytes<0>(o.raw[0], o.raw[1], o.raw[2], o.raw[3], sc[0]);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) acc[rb][0] = mfma_32x32x16(o.a[rb], b0, acc[rb][0]);
-    const bf16x8 b1 = operand_from_bytes<1>(o.raw[0], o.raw[1], o.raw[2], o.raw[3], s1);
+      for (int rb = 0; rb < RB; ++rb) acc[rb][0] = mfma_32x32x16(o.a[rb], b0, acc[rb][0]);
+      const bf16x8 b1 = operand_from_bytes<1>(o.raw[0], o.raw[1], o.raw[2], o.raw[3], sc[1]);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) acc[rb][1] = mfma_32x32x16(o.a[rb], b1, acc[rb][1]);
-    const bf16x8 b2 = operand_from_bytes<2>(o.raw[0], o.raw[1], o.raw[2], o.raw[3], s2);
+      for (int rb = 0; rb < RB; ++rb) acc[rb][1] = mfma_32x32x16(o.a[rb], b1, acc[rb][1]);
+      const bf16x8 b2 = operand_from_bytes<2>(o.raw[0], o.raw[1], o.raw[2], o.raw[3], sc[2]);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) acc[rb][2] = mfma_32x32x16(o.a[rb], b2, acc[rb][2]);
-    const bf16x8 b3 = operand_from_bytes<3>(o.raw[0], o.raw[1], o.raw[2], o.raw[3], s3);
+      for (int rb = 0; rb < RB; ++rb) acc[rb][2] = mfma_32x32x16(o.a[rb], b2, acc[rb][2]);
+      const bf16x8 b3 = operand_from_bytes<3>(o.raw[0], o.raw[1], o.raw[2], o.raw[3], sc[3]);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) acc[rb][3] = mfma_32x32x16(o.a[rb], b3, acc[rb][3]);
+      for (int rb = 0; rb < RB; ++rb) acc[rb][3] = mfma_32x32x16(o.a[rb], b3, acc[rb][3]);
+    } else {
+      u32x4 v0, v1;
+      v0.x = fp4x2_to_bf16x2<0>(o.raw[0], sc[0]);
+      v0.y = fp4x2_to_bf16x2<2>(o.raw[0], sc[0]);
+      v0.z = fp4x2_to_bf16x2<0>(o.raw[1], sc[0]);
+      v0.w = fp4x2_to_bf16x2<2>(o.raw[1], sc[0]);
+      const bf16x8 b0 = __builtin_bit_cast(bf16x8, v0);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) acc[rb][0] = mfma_32x32x16(o.a[rb], b0, acc[rb][0]);
+      v1.x = fp4x2_to_bf16x2<1>(o.raw[0], sc[1]);
+      v1.y = fp4x2_to_bf16x2<3>(o.raw[0], sc[1]);
+      v1.z = fp4x2_to_bf16x2<1>(o.raw[1], sc[1]);
+      v1.w = fp4x2_to_bf16x2<3>(o.raw[1], sc[1]);
+      const bf16x8 b1 = __builtin_bit_cast(bf16x8, v1);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) acc[rb][1] = mfma_32x32x16(o.a[rb], b1, acc[rb][1]);
+    }
   };
-  auto mma_nk = [&](const SubOps<kLayoutNK, RB>& o, const u32x4 (&raw)[4], const float (&sf)[4], int s) {
+  auto mma_nk = [&](const Ops& o, const u32x4 (&raw)[WNC], const float (&sf)[WNC], int s) {
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
+    for (int cb = 0; cb < WNC; ++cb) {
       const bf16x8 b = operand_from_word(raw[cb][s], sf[cb]);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) acc[rb][cb] = mfma_32x32x16(o.a[rb], b, acc[rb][cb]);
@@ -231,86 +282,94 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
   };
 
   if (T > 0) {
-    // prologue: stages 0 and 1 in flight, scales of stage 0
+    // prologue: stages 0 .. NS-2 in flight, scales of stage 0
     uint32_t sc_cur[4] = {0u, 0u, 0u, 0u}, sc_nxt[4] = {0u, 0u, 0u, 0u};
-    load_stage(0, s_begin);
-    if (T > 1) load_stage(1, s_begin + 1);
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st)
+      if (st < T) load_stage(st, s_begin + st);
     load_scales(sc_cur, s_begin);
     wait_vmcnt0();
     __syncthreads();
     Ops cur, nxt;
-    u32x4 braw_cur[4], braw_nxt[4];
+    u32x4 braw_cur[WNC], braw_nxt[WNC];
     read_ops(0, 0, cur);
     if constexpr (LAYOUT == kLayoutNK) read_braw(0, braw_cur);
 
     for (int t = 0; t < T; ++t) {
-      const int buf = t % kStages;
-      const bool more2 = t + 2 < T, more1 = t + 1 < T;
-      if (more2) load_stage((t + 2) % kStages, s_begin + t + 2);
+      const int buf = t % NS;
+      const bool more_far = t + NS - 1 < T, more1 = t + 1 < T;
+      if (more_far) load_stage((t + NS - 1) % NS, s_begin + t + NS - 1);
       if (more1) load_scales(sc_nxt, s_begin + t + 1);
-      float sf[4];
+      float sf[WNC];       // [N,K/2]: per column block
+      float skn[2][WNC];   // [K/2,N]: per K group, per byte column
       if constexpr (LAYOUT == kLayoutNK) {
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) sf[cb] = e8m0_to_f32(sc_cur[cb]);
+        for (int cb = 0; cb < WNC; ++cb) sf[cb] = e8m0_to_f32(sc_cur[cb]);
+      } else {
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+          for (int j = 0; j < WNC; ++j) skn[g][j] = e8m0_to_f32(sc_cur[g] >> (8 * j));
       }
 #pragma unroll
       for (int ks = 0; ks < 3; ++ks) {
         read_ops(buf, ks + 1, nxt);
         if constexpr (LAYOUT == kLayoutKN)
-          mma_kn(cur, sc_cur[ks >> 1]);
+          mma_kn(cur, skn[ks >> 1]);
         else
           mma_nk(cur, braw_cur, sf, ks);
         cur = nxt;
       }
-      // Publish stage t+1: this wave's loads for it were issued one iteration
-      // earlier; only this iteration's VMEM may still be in flight.
-      if (more2 && more1)
-        wait_vmcnt<Cfg::VM_PER_ITER>();
+      // Publish stage t+1: this wave's loads for it were issued NS-2
+      // iterations ago; the VMEM issued since may stay in flight.  Near the
+      // end of the K range fewer loads were issued: wait for all there.
+      if (more_far)
+        wait_vmcnt<(NS - 2) * Cfg::VM_PER_ITER>();
       else
         wait_vmcnt0();
       __syncthreads();
       if (more1) {
-        read_ops((t + 1) % kStages, 0, nxt);
-        if constexpr (LAYOUT == kLayoutNK) read_braw((t + 1) % kStages, braw_nxt);
+        read_ops((t + 1) % NS, 0, nxt);
+        if constexpr (LAYOUT == kLayoutNK) read_braw((t + 1) % NS, braw_nxt);
       }
       if constexpr (LAYOUT == kLayoutKN)
-        mma_kn(cur, sc_cur[1]);
+        mma_kn(cur, skn[1]);
       else
         mma_nk(cur, braw_cur, sf, 3);
       cur = nxt;
       if constexpr (LAYOUT == kLayoutNK) {
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) braw_cur[cb] = braw_nxt[cb];
+        for (int cb = 0; cb < WNC; ++cb) braw_cur[cb] = braw_nxt[cb];
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) sc_cur[i] = sc_nxt[i];
     }
   }
 
-  // ---- split-K fix-up (as tiled_kernel) --------------------------------------
+  // ---- split-K fix-up (same protocol as tiled_kernel) -------------------------
   if (p.splits > 1) {
-    constexpr int Q = RB * 16;
+    constexpr int Q = RB * WNC * 4;  // f32x4 quads per thread
     constexpr uint32_t SLOT = (uint32_t)Q * NT * 16;
     const __amdgpu_buffer_rsrc_t rp =
         make_rsrc(reinterpret_cast<uint8_t*>(p.partials) + (size_t)tile * p.splits * SLOT);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < WNC; ++j)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const f32x4 v = {acc[rb][j][q4 * 4 + 0], acc[rb][j][q4 * 4 + 1], acc[rb][j][q4 * 4 + 2],
                            acc[rb][j][q4 * 4 + 3]};
-          store_coherent(rp, split * SLOT + (uint32_t)(((rb * 4 + j) * 4 + q4) * NT + threadIdx.x) * 16, v);
+          store_coherent(rp, split * SLOT + (uint32_t)(((rb * WNC + j) * 4 + q4) * NT + threadIdx.x) * 16, v);
         }
-    if (!splitk_arrive_last(p.counters + tile, (uint32_t)p.splits, &s_last)) return;
+    if (!splitk_arrive_last(p.counters + tile, (uint32_t)p.splits, s_last)) return;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < WNC; ++j)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-          const uint32_t off = (uint32_t)(((rb * 4 + j) * 4 + q4) * NT + threadIdx.x) * 16;
+          const uint32_t off = (uint32_t)(((rb * WNC + j) * 4 + q4) * NT + threadIdx.x) * 16;
           f32x4 sum = load_coherent4(rp, off);
           for (int sp = 1; sp < p.splits; ++sp) sum += load_coherent4(rp, sp * SLOT + off);
 #pragma unroll
@@ -326,19 +385,30 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
       const int row = m0 + wm * RB * 32 + rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
       if (row >= M) continue;
       if constexpr (LAYOUT == kLayoutKN) {
-        const int col = n0 + wn * 128 + 4 * c;
+        const int col = n0 + wn * WCOLS + WNC * c;
         if (col >= N) continue;
-        if (p.out_bf16) {
-          u32x2 v = {pack_bf16x2(acc[rb][0][i], acc[rb][1][i]), pack_bf16x2(acc[rb][2][i], acc[rb][3][i])};
-          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = v;
+        if constexpr (WNC == 4) {
+          if (p.out_bf16) {
+            u32x2 v = {pack_bf16x2(acc[rb][0][i], acc[rb][1][i]), pack_bf16x2(acc[rb][2][i], acc[rb][3][i])};
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = v;
+          } else {
+            f32x4 v = {acc[rb][0][i], acc[rb][1][i], acc[rb][2][i], acc[rb][3][i]};
+            *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col) = v;
+          }
         } else {
-          f32x4 v = {acc[rb][0][i], acc[rb][1][i], acc[rb][2][i], acc[rb][3][i]};
-          *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col) = v;
+          if (p.out_bf16) {
+            *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) =
+                pack_bf16x2(acc[rb][0][i], acc[rb][1][i]);
+          } else {
+            typedef float f32x2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<f32x2*>(static_cast<float*>(p.C) + (size_t)row * N + col) =
+                f32x2{acc[rb][0][i], acc[rb][1][i]};
+          }
         }
       } else {
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-          const int col = n0 + wn * 128 + 32 * cb + c;
+        for (int cb = 0; cb < WNC; ++cb) {
+          const int col = n0 + wn * WCOLS + 32 * cb + c;
           if (col >= N) continue;
           if (p.out_bf16)
             static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(acc[rb][cb][i]);
@@ -350,20 +420,34 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
   }
 }
 
-template <int LAYOUT, int WM, int WN, int RB>
+template <int LAYOUT, int WM, int WN, int RB, int WNC, int NS>
 hipError_t launch_one(const TiledArgs& a, hipStream_t stream) {
-  using Cfg = PipeCfg<LAYOUT, WM, WN, RB>;
+  using Cfg = PipeCfg<LAYOUT, WM, WN, RB, WNC>;
   const int grid = a.tiles_m * a.tiles_n * a.splits;
-  hipLaunchKernelGGL((tiled_pipe_kernel<LAYOUT, WM, WN, RB>), dim3(grid), dim3(Cfg::NT), 0, stream, a);
+  hipLaunchKernelGGL((tiled_pipe_kernel<LAYOUT, WM, WN, RB, WNC, NS>), dim3(grid), dim3(Cfg::NT), 0,
+                     stream, a);
   return hipGetLastError();
 }
 
+// (wm, wn, rb, wnc, stages) instantiated for both layouts.
+#define MXFP4_PIPE_SHAPES(X) \
+  X(4, 2, 2, 4, 3)           \
+  X(4, 2, 2, 4, 4)           \
+  X(2, 4, 4, 2, 4)           \
+  X(2, 4, 4, 2, 3)           \
+  X(2, 2, 2, 4, 3)           \
+  X(2, 2, 2, 4, 4)           \
+  X(2, 4, 2, 2, 4)           \
+  X(1, 4, 4, 2, 4)           \
+  X(2, 1, 2, 4, 4)
+
 template <int LAYOUT>
 hipError_t dispatch_shape(const TiledShape& s, const TiledArgs& a, hipStream_t stream) {
-  if (s.wm == 4 && s.wn == 2 && s.rb == 2) return launch_one<LAYOUT, 4, 2, 2>(a, stream);
-  if (s.wm == 2 && s.wn == 2 && s.rb == 2) return launch_one<LAYOUT, 2, 2, 2>(a, stream);
-  if (s.wm == 2 && s.wn == 2 && s.rb == 4) return launch_one<LAYOUT, 2, 2, 4>(a, stream);
-  if (s.wm == 2 && s.wn == 1 && s.rb == 2) return launch_one<LAYOUT, 2, 1, 2>(a, stream);
+#define X(WM_, WN_, RB_, WNC_, NS_)                                                     \
+  if (s.wm == WM_ && s.wn == WN_ && s.rb == RB_ && s.wnc == WNC_ && s.stages == NS_) \
+    return launch_one<LAYOUT, WM_, WN_, RB_, WNC_, NS_>(a, stream);
+  MXFP4_PIPE_SHAPES(X)
+#undef X
   return hipErrorInvalidValue;
 }
 
@@ -371,8 +455,11 @@ hipError_t dispatch_shape(const TiledShape& s, const TiledArgs& a, hipStream_t s
 
 bool tiled_pipe_shape_available(int layout, const TiledShape& s) {
   (void)layout;
-  return (s.wm == 4 && s.wn == 2 && s.rb == 2) || (s.wm == 2 && s.wn == 2 && s.rb == 2) ||
-         (s.wm == 2 && s.wn == 2 && s.rb == 4) || (s.wm == 2 && s.wn == 1 && s.rb == 2);
+#define X(WM_, WN_, RB_, WNC_, NS_) \
+  if (s.wm == WM_ && s.wn == WN_ && s.rb == RB_ && s.wnc == WNC_ && s.stages == NS_) return true;
+  MXFP4_PIPE_SHAPES(X)
+#undef X
+  return false;
 }
 
 hipError_t launch_tiled_pipe(int layout, const TiledShape& shape, const TiledArgs& args,

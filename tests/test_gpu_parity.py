@@ -121,7 +121,7 @@ def test_generic_kernel_odd_n(kk):
         assert mo.strict_violations(out, ref, K) == 0
 
 
-TILED_VARIANTS = range(10)
+TILED_VARIANTS = range(15)
 GEMV_VARIANTS = range(15)
 
 
