@@ -11,10 +11,13 @@ them.  The K timed steps are captured once in a HIP graph (no host gaps
 between launches) and replayed between two HIP events on the launch stream;
 ms_per_step = elapsed / K.  Eager (per-call Python) timing is reported next
 to it.  The CPU baseline is the reference CPU path (torch dequant +
-torch.matmul in fp32, python/mxfp4_cdna3/ref.py:75-78) timed on a bounded
-row sample of the same workload with every host core.
+torch.matmul in fp32, python/mxfp4_cdna3/ref.py:75-78) on the same workload,
+repeated for ~10 s with every host core (median reported).  roofline.traffic
+is read from the committed rocprofv3 summary of the same kernel and workload
+(profiles/<kernel>_<workload>.md: FETCH_SIZE + WRITE_SIZE, copy-calibrated).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout kn|nk]
+                       [--no-cpu] [--no-decode] [--calibrate-copy]
 """
 
 import argparse
@@ -105,8 +108,8 @@ def measure(kk, cfg, layout, steps, warmup, plan=None):
     return {"ms": graph_ms, "eager_ms": eager_ms, "rotation_sets": rot, "plan": desc}
 
 
-def cpu_baseline(cfg, target_s=5.0):
-    """Reference CPU path on a row sample of the workload (torch, all host cores)."""
+def cpu_baseline(cfg, budget_s=10.0):
+    """Reference CPU path on the full workload, repeated for ~budget_s (median)."""
     import torch
 
     sys.path.insert(0, REPO)
@@ -119,25 +122,50 @@ def cpu_baseline(cfg, target_s=5.0):
     Bkn, Skn = mo.nk_to_kn(W, S)
     A_t = torch.from_numpy(A_bits.view(np.int16)).view(torch.bfloat16)
 
-    def run(rows):
+    def run():
         t0 = time.perf_counter()
-        mo.ref_gemm_torch(A_t[:rows], Bkn, Skn, mo.LAYOUT_KN)
+        mo.ref_gemm_torch(A_t, Bkn, Skn, mo.LAYOUT_KN)
         return time.perf_counter() - t0
 
-    run(32)
-    t32 = run(32)
-    rows = int(min(M, max(32, 32 * target_s / max(t32, 1e-3))))
-    times = sorted(run(rows) for _ in range(3))
-    t = times[1]
-    tflops = 2.0 * rows * N * K / t / 1e12
+    run()  # warmup
+    times, t_start = [], time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 200):
+        times.append(run())
+    t = sorted(times)[len(times) // 2]
     return {
-        "value": round(tflops, 4),
+        "value": round(2.0 * M * N * K / t / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{rows} of {M} rows of {cfg['name']} ({rows}x{N}x{K}), torch fp32 dequant + "
-                  f"matmul per call, median of 3 ({t:.2f} s each)",
+        "sample": f"full {cfg['name']} workload {M}x{N}x{K} (torch fp32 dequant + matmul per call, as "
+                  f"ref.py:75-78), {len(times)} runs in {sum(times):.1f} s, median {t:.3f} s",
     }
+
+
+def profile_traffic(name):
+    """traffic_bytes_per_launch from a committed rocprofv3 summary (profiles/<name>.md)."""
+    path = os.path.join(REPO, "profiles", name + ".md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if "traffic_bytes_per_launch" in line:
+                    return int(float(line.split("=")[1]))
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
+def copy_calibration(nbytes=1 << 30):
+    """A plain device copy of known size on a cold source (for PMC byte-counter scales)."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(3)
+    flush = torch.empty(2 * nbytes, dtype=torch.uint8, device="cuda").fill_(5)  # evict src from L2
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del flush
 
 
 def main():
@@ -148,6 +176,8 @@ def main():
     ap.add_argument("--layout", choices=["kn", "nk"], default="kn")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode HBM leg")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a cold 1 GiB device copy (scale for PMC byte counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -199,29 +229,33 @@ def main():
     }
 
     if not args.no_decode:
-        dec = measure(kk, DECODE, "nk" if args.layout == "nk" else "kn", max(args.steps, 200), args.warmup)
-        dec_nk = measure(kk, DECODE, "nk", max(args.steps, 200), args.warmup) if args.layout == "kn" else None
         dbytes = gemm_bytes(DECODE["M"], DECODE["N"], DECODE["K"])
-        gbps = dbytes / (dec["ms"] * 1e-3) / 1e9
+        legs = {}
+        for lay in ("nk", "kn"):
+            d = measure(kk, DECODE, lay, max(args.steps, 200), args.warmup)
+            gbps = dbytes / (d["ms"] * 1e-3) / 1e9
+            legs[lay] = (d, gbps)
+        d, gbps = legs["nk"]
         result["hbm_decode"] = {
-            "metric": "HBM GB/s at M=16, N=K=8192",
+            "metric": "HBM GB/s at M=16, N=K=8192 (weights [N,K/2] as in the BASELINE configs)",
             "value": round(gbps, 1),
             "unit": "GB/s",
             "pct_hbm_peak": round(100.0 * gbps / PEAK_HBM_GBPS, 2),
-            "us_per_step": round(dec["ms"] * 1e3, 3),
-            "eager_us_per_step": round(dec["eager_ms"] * 1e3, 3),
-            "plan": dec["plan"],
-            "layout": args.layout,
-            "rotation_sets": dec["rotation_sets"],
+            "us_per_step": round(d["ms"] * 1e3, 3),
+            "eager_us_per_step": round(d["eager_ms"] * 1e3, 3),
+            "plan": d["plan"],
+            "rotation_sets": d["rotation_sets"],
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
                          "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
-                         "bytes_per_launch": dbytes, "traffic": None},
+                         "bytes_per_launch": dbytes, "traffic": profile_traffic("gemv_decode_m16_nk")},
+            "kn_layout": {"value": round(legs["kn"][1], 1), "us_per_step": round(legs["kn"][0]["ms"] * 1e3, 3),
+                          "plan": legs["kn"][0]["plan"],
+                          "traffic": profile_traffic("gemv_decode_m16_kn")},
         }
-        if dec_nk is not None:
-            g2 = dbytes / (dec_nk["ms"] * 1e-3) / 1e9
-            result["hbm_decode"]["nk_layout"] = {"value": round(g2, 1), "us_per_step": round(dec_nk["ms"] * 1e3, 3),
-                                                 "plan": dec_nk["plan"]}
 
+    result["roofline"]["traffic"] = profile_traffic(f"tiled_dit_up_{args.layout}")
+    if args.calibrate_copy:
+        copy_calibration()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(UP)
     else:
