@@ -44,12 +44,12 @@ def _find_db(path: str) -> str | None:
 
 
 def kernel_durations(path: str) -> dict[str, list[float]]:
-    """{kernel name: [duration ns, ...]} from a rocpd db or kernel_trace.csv."""
+    """{kernel name: [duration ns, ...] in dispatch order} from a rocpd db or kernel_trace.csv."""
     out: dict[str, list[float]] = {}
     db = _find_db(path)
     if db:
         con = sqlite3.connect(db)
-        for name, dur in con.execute("select name, duration from kernels"):
+        for name, dur in con.execute("select name, duration from kernels order by start"):
             out.setdefault(name, []).append(float(dur))
         return out
     csvs = sorted(glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True))
@@ -63,14 +63,15 @@ def kernel_durations(path: str) -> dict[str, list[float]]:
     return out
 
 
-def counters(path: str) -> dict[str, dict[str, float]]:
-    """{kernel name: {counter: mean value per dispatch}} from a rocpd db."""
+def counters(path: str, reduce: str = "avg") -> dict[str, dict[str, float]]:
+    """{kernel name: {counter: value per dispatch}} from a rocpd db; reduce = avg | max."""
     db = _find_db(path)
     if not db:
         return {}
     con = sqlite3.connect(db)
+    fn = {"avg": "avg", "max": "max"}[reduce]
     rows = con.execute(
-        "select kernel_name, counter_name, avg(value) from counters_collection "
+        f"select kernel_name, counter_name, {fn}(value) from counters_collection "
         "group by kernel_name, counter_name").fetchall()
     out: dict[str, dict[str, float]] = {}
     for kname, cname, val in rows:
@@ -84,10 +85,15 @@ def _select(names, regex):
 
 
 def summarize(trace: str, kernel_re: str, pmc: list[str], copy_bytes: float | None,
-              flops: float | None, alg_bytes: float | None, title: str, command: str) -> tuple[str, dict]:
+              flops: float | None, alg_bytes: float | None, title: str, command: str,
+              last: int | None = None) -> tuple[str, dict]:
     durs = kernel_durations(trace)
+    if last:
+        durs = {k: v[-last:] for k, v in durs.items()}
     sel = _select(durs, kernel_re)
     lines = [f"# {title}", "", f"command: `{command}`" if command else "", ""]
+    if last:
+        lines += [f"durations: the last {last} dispatches of each kernel (the timed graph replay)", ""]
     lines += ["| kernel | dispatches | avg us | median us | min us | max us |", "|---|---|---|---|---|---|"]
     result: dict = {}
     all_d = []
@@ -114,8 +120,10 @@ def summarize(trace: str, kernel_re: str, pmc: list[str], copy_bytes: float | No
         c = counters(db)
         for n in _select(c, kernel_re):
             merged.update(c[n])
-        for n in _select(c, COPY_KERNEL_RE):
-            copy_c.update(c[n])
+        # calibration copy = the largest copy dispatch (the run also copies smaller buffers)
+        cmax = counters(db, "max")
+        for n in _select(cmax, COPY_KERNEL_RE):
+            copy_c.update(cmax[n])
     if merged:
         lines += ["", "## counters (mean per dispatch)", "", "| counter | value |", "|---|---|"]
         for k in sorted(merged):
@@ -153,8 +161,10 @@ def main(argv=None):
     ap.add_argument("--title", default="rocprofv3 summary")
     ap.add_argument("--command", default="")
     ap.add_argument("--out", default=None)
+    ap.add_argument("--last", type=int, default=None, help="only the last N dispatches of each kernel")
     a = ap.parse_args(argv)
-    text, _ = summarize(a.trace, a.kernel, a.pmc, a.copy_bytes, a.flops, a.alg_bytes, a.title, a.command)
+    text, _ = summarize(a.trace, a.kernel, a.pmc, a.copy_bytes, a.flops, a.alg_bytes, a.title, a.command,
+                        a.last)
     if a.out:
         with open(a.out, "w") as f:
             f.write(text)
