@@ -42,8 +42,8 @@ const TiledVariant kTiled[] = {
     {{1, 2, 1}, 0.20, 0.17, 4, false},        // 5:  32 x 256
     {{4, 2, 2, 4, 3}, 0.433, 0.336, 1, true}, // 6: pipelined 256 x 256, 8 waves of 64 x 128, 3 stages
     {{2, 2, 2, 4, 3}, 0.32, 0.23, 1, true},   // 7: pipelined 128 x 256, 4 waves of 64 x 128
-    {{4, 2, 2, 4, 4}, 0.432, 0.333, 1, true}, // 8: as 6 with a 4-stage ring (160 KB)
-    {{2, 4, 4, 2, 4}, 0.38, 0.369, 1, true},  // 9: pipelined 256 x 256, 8 waves of 128 x 64, 4 stages
+    {{4, 2, 2, 4, 3}, 0.432, 0.333, 1, true}, // 8: = 6 (a 4-stage 256 x 256 ring no longer fits 160 KB)
+    {{2, 4, 4, 2, 3}, 0.37, 0.361, 1, true},  // 9: = 10
     {{2, 4, 4, 2, 3}, 0.37, 0.361, 1, true},  // 10: as 9 with 3 stages
     {{2, 2, 2, 4, 4}, 0.33, 0.23, 1, true},   // 11: as 7 with 4 stages
     {{2, 4, 2, 2, 4}, 0.31, 0.26, 1, true},   // 12: pipelined 128 x 256, 8 waves of 64 x 64
@@ -127,6 +127,7 @@ void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) 
   const int64_t ksteps = ceil_div(K, 64);
   for (int v = 0; v < kNumTiled; ++v) {
     const TiledVariant& tv = kTiled[v];
+    if (tv.pipe && layout == kLayoutNK && K % 128 != 0) continue;
     const int64_t tiles = ceil_div(M, tv.shape.bm()) * ceil_div(N, tv.shape.bn());
     for (int s = 1; s <= 16 && s <= ksteps; ++s) {
       if (s > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) break;
@@ -160,6 +161,8 @@ hipError_t validate_plan(int layout, int64_t M, int64_t N, int64_t K, const mxfp
     case MXFP4_KERNEL_TILED: {
       if (p.variant < 0 || p.variant >= kNumTiled) return hipErrorInvalidValue;
       if (layout == kLayoutKN && N % 16 != 0) return hipErrorInvalidValue;
+      // the pipelined kernel reads [N,K/2] scales as aligned dwords of 4 groups
+      if (kTiled[p.variant].pipe && layout == kLayoutNK && K % 128 != 0) return hipErrorInvalidValue;
       const TiledShape& s = kTiled[p.variant].shape;
       const int64_t tiles = ceil_div(M, s.bm()) * ceil_div(N, s.bn());
       if (p.split_k > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) return hipErrorInvalidValue;

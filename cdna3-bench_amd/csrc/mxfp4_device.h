@@ -95,6 +95,43 @@ __device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, v
 
 __device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// s_waitcnt vmcnt(N) with expcnt/lgkmcnt left at their maxima (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// ---- LDS DMA issued as inline asm ---------------------------------------------
+// The compiler treats every LDS read that follows a buffer_load ... lds it
+// can see as possibly aliasing it and waits for vmcnt(0) first (it has no
+// alias information for one LDS array), which drains a multi-stage ring on
+// every step.  The ring kernels therefore issue their global->LDS loads as
+// asm the compiler does not track, count them themselves (wait_vmcnt<N>
+// before the barrier that publishes a stage) and keep no compiler-visible
+// VMEM loads inside the pipelined loop: a compiler-computed vmcnt would not
+// count these loads and would drain the ring again.
+typedef uint32_t desc_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor over [base, base + num_records) (stride 0, 32-bit
+// data format, as __builtin_amdgcn_make_buffer_rsrc builds it).  base and
+// num_records must be wave-uniform.
+__device__ __forceinline__ desc_t make_desc(const void* base, uint32_t num_records = kNumRecords) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  return desc_t{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, num_records, 0x00020000u};
+}
+
+// 16 bytes per lane: global (desc + voffset) -> LDS lds + 16 * lane.
+__device__ __forceinline__ void dma16(desc_t d, const void* lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"((uint32_t)(uintptr_t)lds), "v"(voffset), "s"(d) : "memory", "m0");
+}
+// 4 bytes per lane: global (desc + voffset) -> LDS lds + 4 * lane.
+__device__ __forceinline__ void dma4(desc_t d, const void* lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :: "s"((uint32_t)(uintptr_t)lds), "v"(voffset), "s"(d) : "memory", "m0");
+}
+
 // Split-K partials cross XCDs, whose L2s are not coherent with each other.
 // Instead of __threadfence() (buffer_wbl2 + buffer_inv of the whole L2 on
 // gfx950, which flushes every CTA's cached tiles), the partials themselves

@@ -37,13 +37,6 @@ constexpr int kBK = 64;
 
 __device__ __forceinline__ int a_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-// s_waitcnt vmcnt(N) with expcnt/lgkmcnt left at their maxima (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 template <int LAYOUT, int WM, int WN, int RB, int WNC>
 struct PipeCfg {
   static constexpr int NWAVES = WM * WN;
@@ -53,15 +46,20 @@ struct PipeCfg {
   static constexpr int BN = WN * WCOLS;
   static constexpr int A_BYTES = BM * 128;
   static constexpr int B_BYTES = BN * 32;
-  static constexpr int STAGE = A_BYTES + B_BYTES;
+  // E8M0 scales of a stage also go through LDS: [K/2,N]: the stage's two K
+  // group rows of BN bytes; [N,K/2]: per column the aligned dword holding its
+  // two groups (needs K % 128 == 0).  One 64-lane x 4-byte DMA per wave.
+  static constexpr int SC_BYTES = LAYOUT == kLayoutKN ? 2 * BN : 4 * BN;
+  static constexpr int SC_INSTR = SC_BYTES / 256;
+  static constexpr int STAGE = A_BYTES + B_BYTES + SC_BYTES;
   static constexpr int A_INSTR = A_BYTES / 1024;
   static constexpr int B_INSTR = B_BYTES / 1024;
   static_assert(A_INSTR % NWAVES == 0 && B_INSTR % NWAVES == 0, "loads split evenly over waves");
   static constexpr int A_PER_WAVE = A_INSTR / NWAVES;
   static constexpr int B_PER_WAVE = B_INSTR / NWAVES;
-  static constexpr int SC_LOADS = LAYOUT == kLayoutKN ? 2 : WNC;
-  // VMEM instructions one wave issues per iteration (one stage + next scales).
-  static constexpr int VM_PER_ITER = A_PER_WAVE + B_PER_WAVE + SC_LOADS;
+  static_assert(SC_INSTR >= 1 && SC_INSTR <= NWAVES, "one scale DMA per wave");
+  // LDS DMAs one wave issues per stage (A, B, one scale DMA).
+  static constexpr int VM_PER_ITER = A_PER_WAVE + B_PER_WAVE + 1;
   static constexpr int KN_CPR = BN / 16;  // 16-byte chunks per K-pair row
 };
 
@@ -85,8 +83,11 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
   constexpr int NT = Cfg::NT, BM = Cfg::BM, BN = Cfg::BN, WCOLS = Cfg::WCOLS;
   static_assert(NS >= 3, "the barrier placement needs at least three stages");
   static_assert(WNC == 2 || WNC == 4, "wave column width");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * Cfg::STAGE];
-  int* s_last = reinterpret_cast<int*>(smem);  // split-K flag; the ring is dead by then
+  static_assert(NS * Cfg::STAGE + 256 <= 160 * 1024, "LDS ring exceeds 160 KB");
+  // NS stages, then a 256-byte window that the scale DMAs of waves beyond
+  // SC_INSTR fill (so every wave issues the same DMA count per stage).
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * Cfg::STAGE + 256];
+  int* s_last = reinterpret_cast<int*>(smem);  // split-K flag; the ring has drained by then
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
@@ -112,22 +113,22 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
   const int T = min(p.ksteps, s_begin + p.steps_per_split) - s_begin;
 
   // ---- global -> LDS ---------------------------------------------------------
-  auto load_stage = [&](int buf, int step) {
+  auto load_stage = [&](int buf, int step, bool live) {
     uint8_t* sA = smem + buf * Cfg::STAGE;
     uint8_t* sB = sA + Cfg::A_BYTES;
     const int k0 = step * kBK;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A + (size_t)m0 * K + k0);
+    const desc_t ra = make_desc(p.A + (size_t)m0 * K + k0);
 #pragma unroll
     for (int ii = 0; ii < Cfg::A_PER_WAVE; ++ii) {
       const int i = wave * Cfg::A_PER_WAVE + ii;
       const int row = i * 8 + (lane >> 3);
       const int lc = (lane & 7) ^ a_swz(row);
-      const bool ok = (m0 + row < M) && (k0 + lc * 8 < K);
-      buffer_load_lds16(ra, sA + i * 1024, ok ? (uint32_t)(row * K * 2 + lc * 16) : kOobOffset);
+      const bool ok = live && (m0 + row < M) && (k0 + lc * 8 < K);
+      dma16(ra, sA + i * 1024, ok ? (uint32_t)(row * K * 2 + lc * 16) : kOobOffset);
     }
     if constexpr (LAYOUT == kLayoutKN) {
       constexpr int CPR = Cfg::KN_CPR;
-      const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B + (size_t)(k0 >> 1) * N + n0);
+      const desc_t rb = make_desc(p.B + (size_t)(k0 >> 1) * N + n0);
 #pragma unroll
       for (int ii = 0; ii < Cfg::B_PER_WAVE; ++ii) {
         const int i = wave * Cfg::B_PER_WAVE + ii;
@@ -135,45 +136,36 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
         const int row = q / CPR;
         // rows with bit 2 set store their two row halves swapped
         const int lc = (q % CPR) ^ (((row >> 2) & 1) * (CPR / 2));
-        const bool ok = ((k0 >> 1) + row < Kh) && (n0 + lc * 16 < N);
-        buffer_load_lds16(rb, sB + i * 1024, ok ? (uint32_t)(row * N + lc * 16) : kOobOffset);
+        const bool ok = live && ((k0 >> 1) + row < Kh) && (n0 + lc * 16 < N);
+        dma16(rb, sB + i * 1024, ok ? (uint32_t)(row * N + lc * 16) : kOobOffset);
       }
     } else {
-      const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B + (size_t)n0 * Kh + (k0 >> 1));
+      const desc_t rb = make_desc(p.B + (size_t)n0 * Kh + (k0 >> 1));
 #pragma unroll
       for (int ii = 0; ii < Cfg::B_PER_WAVE; ++ii) {
         const int i = wave * Cfg::B_PER_WAVE + ii;
         const int q = i * 64 + lane;
         const int row = q >> 1;
         const int lc = (q & 1) ^ ((row >> 2) & 1);  // rows with bit 2 set swap their chunks
-        const bool ok = (n0 + row < N) && ((k0 >> 1) + lc * 16 < Kh);
-        buffer_load_lds16(rb, sB + i * 1024, ok ? (uint32_t)(row * Kh + lc * 16) : kOobOffset);
+        const bool ok = live && (n0 + row < N) && ((k0 >> 1) + lc * 16 < Kh);
+        dma16(rb, sB + i * 1024, ok ? (uint32_t)(row * Kh + lc * 16) : kOobOffset);
       }
     }
-  };
-
-  // Scales straight from global (L2-resident) one stage ahead; exactly
-  // SC_LOADS VMEM instructions per call (masked lanes fetch nothing).
-  auto load_scales = [&](uint32_t (&dst)[4], int step) {
+    // scales: wave w < SC_INSTR loads bytes 256w .. 256w+255 of the stage's scale block
     const int g0 = step * 2;
+    const bool sc_wave = wave < Cfg::SC_INSTR;
+    uint8_t* sC = sB + Cfg::B_BYTES;
     if constexpr (LAYOUT == kLayoutKN) {
-      const bool cok = n0 + wn * WCOLS + WNC * c < N;
-      const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.S + (size_t)g0 * N + n0 + wn * WCOLS);
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const uint32_t off = (cok && g0 + g < G) ? (uint32_t)(g * N + WNC * c) : kOobOffset;
-        if constexpr (WNC == 4)
-          dst[g] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
-        else
-          dst[g] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
-      }
+      const desc_t rs = make_desc(p.S + (size_t)g0 * N + n0);
+      const int byte = 256 * wave + 4 * lane;
+      const int row = byte / BN, col = byte % BN;
+      const bool ok = live && sc_wave && (g0 + row < G) && (n0 + col < N);
+      dma4(rs, sc_wave ? sC + 256 * wave : smem + NS * Cfg::STAGE, ok ? (uint32_t)(row * N + col) : kOobOffset);
     } else {
-      const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.S + (size_t)(n0 + wn * WCOLS) * G + g0);
-#pragma unroll
-      for (int cb = 0; cb < WNC; ++cb) {
-        const bool ok = (g0 + h < G) && (n0 + wn * WCOLS + 32 * cb + c < N);
-        dst[cb] = __builtin_amdgcn_raw_buffer_load_b8(rs, ok ? (uint32_t)((32 * cb + c) * G + h) : kOobOffset, 0, 0);
-      }
+      const desc_t rs = make_desc(p.S + (size_t)n0 * G + (g0 & ~3));
+      const int n = 64 * wave + lane;
+      const bool ok = live && sc_wave && (n0 + n < N) && (g0 < G);
+      dma4(rs, sc_wave ? sC + 256 * wave : smem + NS * Cfg::STAGE, ok ? (uint32_t)(n * G) : kOobOffset);
     }
   };
 
@@ -282,12 +274,11 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
   };
 
   if (T > 0) {
-    // prologue: stages 0 .. NS-2 in flight, scales of stage 0
-    uint32_t sc_cur[4] = {0u, 0u, 0u, 0u}, sc_nxt[4] = {0u, 0u, 0u, 0u};
+    // Every iteration issues the same DMA sequence (stage t+NS-1; ranges past
+    // the split masked to the OOB offset instead of skipped), so one counted
+    // wait per iteration publishes the next stage and leaves NS-2 in flight.
 #pragma unroll
-    for (int st = 0; st < NS - 1; ++st)
-      if (st < T) load_stage(st, s_begin + st);
-    load_scales(sc_cur, s_begin);
+    for (int st = 0; st < NS - 1; ++st) load_stage(st, s_begin + st, st < T);
     wait_vmcnt0();
     __syncthreads();
     Ops cur, nxt;
@@ -297,19 +288,25 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
 
     for (int t = 0; t < T; ++t) {
       const int buf = t % NS;
-      const bool more_far = t + NS - 1 < T, more1 = t + 1 < T;
-      if (more_far) load_stage((t + NS - 1) % NS, s_begin + t + NS - 1);
-      if (more1) load_scales(sc_nxt, s_begin + t + 1);
+      load_stage((t + NS - 1) % NS, s_begin + t + NS - 1, t + NS - 1 < T);
+      // this stage's scales (published with its data)
+      const uint8_t* sC = smem + buf * Cfg::STAGE + Cfg::A_BYTES + Cfg::B_BYTES;
       float sf[WNC];       // [N,K/2]: per column block
       float skn[2][WNC];   // [K/2,N]: per K group, per byte column
       if constexpr (LAYOUT == kLayoutNK) {
+        const int shift = 8 * (((2 * (s_begin + t)) & 2) + h);
 #pragma unroll
-        for (int cb = 0; cb < WNC; ++cb) sf[cb] = e8m0_to_f32(sc_cur[cb]);
+        for (int cb = 0; cb < WNC; ++cb)
+          sf[cb] = e8m0_to_f32(*reinterpret_cast<const uint32_t*>(sC + 4 * (wn * WCOLS + 32 * cb + c)) >> shift);
       } else {
 #pragma unroll
-        for (int g = 0; g < 2; ++g)
+        for (int g = 0; g < 2; ++g) {
+          const uint8_t* row = sC + g * BN + wn * WCOLS + WNC * c;
+          const uint32_t w = WNC == 4 ? *reinterpret_cast<const uint32_t*>(row)
+                                      : (uint32_t)*reinterpret_cast<const uint16_t*>(row);
 #pragma unroll
-          for (int j = 0; j < WNC; ++j) skn[g][j] = e8m0_to_f32(sc_cur[g] >> (8 * j));
+          for (int j = 0; j < WNC; ++j) skn[g][j] = e8m0_to_f32(w >> (8 * j));
+        }
       }
 #pragma unroll
       for (int ks = 0; ks < 3; ++ks) {
@@ -320,18 +317,13 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
           mma_nk(cur, braw_cur, sf, ks);
         cur = nxt;
       }
-      // Publish stage t+1: this wave's loads for it were issued NS-2
-      // iterations ago; the VMEM issued since may stay in flight.  Near the
-      // end of the K range fewer loads were issued: wait for all there.
-      if (more_far)
-        wait_vmcnt<(NS - 2) * Cfg::VM_PER_ITER>();
-      else
-        wait_vmcnt0();
+      // Publish stage t+1: this wave's DMAs for it were issued NS-2 iterations
+      // ago; the ones issued since stay in flight.
+      wait_vmcnt<(NS - 2) * Cfg::VM_PER_ITER>();
       __syncthreads();
-      if (more1) {
-        read_ops((t + 1) % NS, 0, nxt);
-        if constexpr (LAYOUT == kLayoutNK) read_braw((t + 1) % NS, braw_nxt);
-      }
+      // Past the last step this reads a stage of OOB zeros; the values are unused.
+      read_ops((t + 1) % NS, 0, nxt);
+      if constexpr (LAYOUT == kLayoutNK) read_braw((t + 1) % NS, braw_nxt);
       if constexpr (LAYOUT == kLayoutKN)
         mma_kn(cur, skn[1]);
       else
@@ -341,9 +333,10 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
 #pragma unroll
         for (int cb = 0; cb < WNC; ++cb) braw_cur[cb] = braw_nxt[cb];
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc_cur[i] = sc_nxt[i];
     }
+    // The masked DMAs of the last iterations still write the ring.
+    wait_vmcnt0();
+    __syncthreads();
   }
 
   // ---- split-K fix-up (same protocol as tiled_kernel) -------------------------
@@ -432,8 +425,6 @@ hipError_t launch_one(const TiledArgs& a, hipStream_t stream) {
 // (wm, wn, rb, wnc, stages) instantiated for both layouts.
 #define MXFP4_PIPE_SHAPES(X) \
   X(4, 2, 2, 4, 3)           \
-  X(4, 2, 2, 4, 4)           \
-  X(2, 4, 4, 2, 4)           \
   X(2, 4, 4, 2, 3)           \
   X(2, 2, 2, 4, 3)           \
   X(2, 2, 2, 4, 4)           \

@@ -122,20 +122,26 @@ def test_generic_kernel_odd_n(kk):
 
 
 TILED_VARIANTS = range(15)
+PIPE_VARIANTS = range(6, 15)  # pipelined kernel; [N,K/2] needs K % 128 == 0
 GEMV_VARIANTS = range(15)
 
 
-@pytest.mark.parametrize("layout", ["kn", "nk"])
-def test_every_tiled_variant_and_split(kk, layout):
+@pytest.mark.parametrize("layout,K", [("kn", 672), ("nk", 672), ("nk", 640)])
+def test_every_tiled_variant_and_split(kk, layout, K):
     import torch
 
-    M, N, K = 300, 512, 672  # M tail, 2 N tiles at BN=256, K % 64 == 32
+    M, N = 300, 512  # M tail, 2 N tiles at BN=256; K = 672: K % 64 == 32
     A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=21)
     ref = oracle_f64(A_bits, W, S)
     for v in TILED_VARIANTS:
-        for split in (1, 2, 3, 11):
-            log(f"case tiled variant={v} split={split} layout={layout}")
-            out = run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=(kk.KERNEL_TILED, v, split))
+        for split in (1, 2, 3, (K + 63) // 64):  # the last: one 64-K step per split
+            log(f"case tiled variant={v} split={split} layout={layout} K={K}")
+            plan = (kk.KERNEL_TILED, v, split)
+            if layout == "nk" and K % 128 and v in PIPE_VARIANTS:
+                with pytest.raises(RuntimeError, match="invalid argument"):
+                    run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=plan)
+                continue
+            out = run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=plan)
             bad = mo.strict_violations(out, ref, K)
             assert bad == 0, f"variant {v} split {split}: {bad} bad"
 
