@@ -247,7 +247,7 @@ def main():
             "rotation_sets": d["rotation_sets"],
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
                          "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
-                         "bytes_per_launch": dbytes, "traffic": profile_traffic("gemv_decode_m16_nk")},
+                         "bytes_per_launch": dbytes, "traffic": profile_traffic("stream_decode_m16_nk")},
             "kn_layout": {"value": round(legs["kn"][1], 1), "us_per_step": round(legs["kn"][0]["ms"] * 1e3, 3),
                           "plan": legs["kn"][0]["plan"],
                           "traffic": profile_traffic("gemv_decode_m16_kn")},

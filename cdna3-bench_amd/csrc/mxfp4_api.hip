@@ -61,12 +61,39 @@ const GemvShape kGemv[] = {
 };
 constexpr int kNumGemv = sizeof(kGemv) / sizeof(kGemv[0]);
 
+// Shapes of the streaming split-K family ([N,K/2], M <= 32); index =
+// mxfp4_plan.variant.  (mt, waves, gcb, nslot, smax) -- same order as
+// MXFP4_STREAM_SHAPES in mxfp4_stream.hip.  Splits are fixed by the shape:
+// ceil(K / (waves * 256)).
+const StreamShape kStream[] = {
+    {1, 8, 2, 4, 4, 256},  // 0: M <= 16, split 2048 K (K <= 8192)
+    {1, 4, 2, 8, 8, 256},  // 1: M <= 16, split 1024 K (K <= 8192)
+    {2, 4, 2, 8, 8, 256},  // 2: M <= 32, split 1024 K (K <= 8192)
+    {1, 8, 2, 2, 2, 512},  // 3: M <= 16, split 4096 K (K <= 8192)
+    {2, 4, 2, 4, 4, 512},  // 4: M <= 32, split 2048 K (K <= 8192)
+};
+constexpr int kNumStream = sizeof(kStream) / sizeof(kStream[0]);
+constexpr int kStreamSpin = 4096;  // late-unit polls before counter arbitration
+
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 double problem_bytes(int64_t M, int64_t N, int64_t K, int c_bytes) {
   return 2.0 * M * K + N * K / 2.0 + N * K / 32.0 + (double)c_bytes * M * N;
+}
+
+int64_t stream_splits(const StreamShape& s, int64_t K) { return ceil_div(K, s.k_split()); }
+int64_t stream_ctas(const StreamShape& s, int64_t N, int64_t K) {
+  const int64_t splits = stream_splits(s, K);
+  return ceil_div(ceil_div(N, 32), splits) * splits;
+}
+bool stream_plan_ok(int layout, int64_t M, int64_t N, int64_t K, const StreamShape& s) {
+  if (layout != kLayoutNK || M > 16 * s.mt || K % s.kw != 0) return false;
+  const int64_t splits = stream_splits(s, K);
+  if (splits > s.smax) return false;
+  if (splits > 1 && stream_ctas(s, N, K) * 4 > (int64_t)MXFP4_COUNTER_BYTES) return false;
+  return stream_shape_available(s);
 }
 
 int gemv_steps(int layout, int64_t K) { return (int)(layout == kLayoutKN ? K / 32 : ceil_div(K, 128)); }
@@ -86,6 +113,22 @@ bool gemv_plan_ok(int layout, int64_t M, int64_t N, const GemvShape& g) {
 // weight bytes, so S stays small.
 void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
   const bool two = M > 16;
+  // [N,K/2] with enough column groups to fill the chip: the streaming split-K
+  // kernel, first choice that fits (measured on MI355X at N = 8192 / 28672,
+  // K = 8192: 512-K waves with 2 splits beat 256-K waves with 4; both beat
+  // this family by 1.3-1.7x).
+  if (layout == kLayoutNK) {
+    static const int kPrefer16[] = {3, 0, 1}, kPrefer32[] = {4, 2};
+    const int* pref = two ? kPrefer32 : kPrefer16;
+    const int npref = two ? 2 : 3;
+    for (int i = 0; i < npref; ++i) {
+      const StreamShape& st = kStream[pref[i]];
+      if (stream_plan_ok(layout, M, N, K, st) && stream_ctas(st, N, K) >= 192) {
+        *out = {MXFP4_KERNEL_STREAM, pref[i], (int32_t)stream_splits(st, K), 0};
+        return;
+      }
+    }
+  }
   int want;
   if (layout == kLayoutKN)
     want = two ? 4 : 0;  // (2,8,8,2) / (1,8,8,4)
@@ -158,6 +201,14 @@ hipError_t validate_plan(int layout, int64_t M, int64_t N, int64_t K, const mxfp
       if (p.split_k > gemv_steps(layout, K)) return hipErrorInvalidValue;
       return hipSuccess;
     }
+    case MXFP4_KERNEL_STREAM: {
+      if (p.variant < 0 || p.variant >= kNumStream) return hipErrorInvalidValue;
+      const StreamShape& s = kStream[p.variant];
+      if (!stream_plan_ok(layout, M, N, K, s)) return hipErrorInvalidValue;
+      // the split count is fixed by the shape; split_k must restate it
+      if (p.split_k != stream_splits(s, K)) return hipErrorInvalidValue;
+      return hipSuccess;
+    }
     case MXFP4_KERNEL_TILED: {
       if (p.variant < 0 || p.variant >= kNumTiled) return hipErrorInvalidValue;
       if (layout == kLayoutKN && N % 16 != 0) return hipErrorInvalidValue;
@@ -190,6 +241,10 @@ size_t plan_workspace(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_p
   if (p.kernel == MXFP4_KERNEL_GEMV) {
     const GemvShape& g = kGemv[p.variant];
     partial = (size_t)ceil_div(N, 16 * g.cb) * p.split_k * gemv_tile(g) * sizeof(float);
+  } else if (p.kernel == MXFP4_KERNEL_STREAM) {
+    const StreamShape& s = kStream[p.variant];
+    // 8-byte (value, tag) packets per partial element
+    partial = (size_t)stream_ctas(s, N, K) * p.split_k * s.tile() * 8;
   } else if (p.kernel == MXFP4_KERNEL_TILED) {
     const TiledShape& s = kTiled[p.variant].shape;
     const int64_t ksteps = ceil_div(K, 64);
@@ -266,6 +321,20 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
       a.counters = a.splits > 1 ? counters : nullptr;
       return launch_gemv(layout, g, a, stream);
     }
+    case MXFP4_KERNEL_STREAM: {
+      const StreamShape& s = kStream[plan.variant];
+      StreamArgs a{};
+      a.A = A16; a.B = B; a.S = S; a.C = C;
+      a.M = (int)M; a.N = (int)N; a.K = (int)K;
+      a.out_bf16 = out_bf16;
+      a.splits = (int)stream_splits(s, K);
+      a.groups = (int)ceil_div(N, 32);
+      a.ctas = (int)stream_ctas(s, N, K);
+      a.partials = a.splits > 1 ? partials : nullptr;
+      a.counters = a.splits > 1 ? counters : nullptr;
+      a.spin_limit = kStreamSpin;
+      return launch_stream(s, a, stream);
+    }
     case MXFP4_KERNEL_TILED: {
       const TiledShape& s = kTiled[plan.variant].shape;
       TiledArgs a{};
@@ -314,6 +383,13 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
                kGemv[plan->variant].cb, kGemv[plan->variant].wpc, kGemv[plan->variant].u,
                plan->split_k);
       return hipSuccess;
+    case MXFP4_KERNEL_STREAM: {
+      if (plan->variant < 0 || plan->variant >= kNumStream) return hipErrorInvalidValue;
+      const StreamShape& s = kStream[plan->variant];
+      snprintf(buf, buf_len, "stream mt%d w%d kw%d kr%d split%d", s.mt, s.waves, s.kw, s.k_split(),
+               plan->split_k);
+      return hipSuccess;
+    }
     case MXFP4_KERNEL_TILED: {
       if (plan->variant < 0 || plan->variant >= kNumTiled) return hipErrorInvalidValue;
       const TiledShape& s = kTiled[plan->variant].shape;

@@ -102,6 +102,21 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// vmcnt(n) for a wave-uniform n known only at run time (0 <= n < 64; larger n
+// waits for vmcnt(63)).  A branch chain over immediates.
+template <int I = 0>
+__device__ __forceinline__ void wait_vmcnt_rt(int n) {
+  if constexpr (I < 63) {
+    if (n == I) {
+      wait_vmcnt<I>();
+      return;
+    }
+    wait_vmcnt_rt<I + 1>(n);
+  } else {
+    wait_vmcnt<63>();
+  }
+}
+
 // ---- LDS DMA issued as inline asm ---------------------------------------------
 // The compiler treats every LDS read that follows a buffer_load ... lds it
 // can see as possibly aliasing it and waits for vmcnt(0) first (it has no
@@ -122,14 +137,16 @@ __device__ __forceinline__ desc_t make_desc(const void* base, uint32_t num_recor
 }
 
 // 16 bytes per lane: global (desc + voffset) -> LDS lds + 16 * lane.
+// M0 (the LDS base of the DMA) is an input operand, so the compiler writes it
+// and knows the asm reads it.
 __device__ __forceinline__ void dma16(desc_t d, const void* lds, uint32_t voffset) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :: "s"((uint32_t)(uintptr_t)lds), "v"(voffset), "s"(d) : "memory", "m0");
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voffset), "s"(d), "{m0}"((uint32_t)(uintptr_t)lds) : "memory");
 }
 // 4 bytes per lane: global (desc + voffset) -> LDS lds + 4 * lane.
 __device__ __forceinline__ void dma4(desc_t d, const void* lds, uint32_t voffset) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-               :: "s"((uint32_t)(uintptr_t)lds), "v"(voffset), "s"(d) : "memory", "m0");
+  asm volatile("buffer_load_dword %0, %1, 0 offen lds"
+               :: "v"(voffset), "s"(d), "{m0}"((uint32_t)(uintptr_t)lds) : "memory");
 }
 
 // Split-K partials cross XCDs, whose L2s are not coherent with each other.

@@ -74,6 +74,39 @@ hipError_t launch_gemv(int layout, const GemvShape& shape, const GemvArgs& args,
                        hipStream_t stream);
 bool gemv_shape_available(int layout, const GemvShape& shape);
 
+// Streaming split-K family for M <= 32 and [N,K/2] weights (mxfp4_stream.hip):
+// 32-column groups, K in `splits` ranges of waves * kw, one CTA per
+// (group block, split) processing `splits` units; partials travel as tagged
+// packets.
+struct StreamArgs {
+  const uint16_t* A;
+  const uint8_t* B;
+  const uint8_t* S;
+  void* C;
+  int M, N, K;
+  int out_bf16;
+  int splits;           // ceil(K / (waves * 256)), <= smax
+  int groups;           // ceil(N / 32)
+  int ctas;             // ceil(groups / splits) * splits
+  float* partials;      // splits > 1: [ctas][splits][16*mt*32] packets of 8 bytes, zero on entry/exit
+  uint32_t* counters;   // splits > 1: [ctas], zero on entry, zero on exit
+  int spin_limit;       // polls of the late unit before it falls back to counter arbitration
+};
+
+struct StreamShape {
+  int mt;     // 16-row MFMA tiles (1: M <= 16, 2: M <= 32)
+  int waves;  // compute waves per CTA (split = waves * kw K)
+  int gcb;    // 16-column blocks per group (2)
+  int nslot;  // LDS ring units per wave
+  int smax;   // largest split count of this instantiation
+  int kw;     // K per compute wave and unit (256 or 512)
+  int k_split() const { return waves * kw; }
+  int tile() const { return 16 * mt * 16 * gcb; }
+};
+
+hipError_t launch_stream(const StreamShape& shape, const StreamArgs& args, hipStream_t stream);
+bool stream_shape_available(const StreamShape& shape);
+
 // Any shape with K % 32 == 0; one thread per output, for shapes the fast
 // families do not cover (N % 16 != 0).
 hipError_t launch_generic(int layout, const uint16_t* A, const uint8_t* B, const uint8_t* S,

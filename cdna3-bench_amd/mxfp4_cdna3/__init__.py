@@ -15,7 +15,7 @@ _KERNEL_NAMES = (
     "gemm_i", "gemm_j", "gemm_k", "gemm_m", "gemm_auto", "gemm", "dequantize",
     "select_plan", "device_info", "shape_supported_c", "shape_supported_d",
     "shape_supported_e", "shape_supported_f", "shape_supported_g", "version",
-    "LAYOUT_KN", "LAYOUT_NK", "KERNEL_AUTO", "KERNEL_GEMV", "KERNEL_TILED", "KERNEL_GENERIC",
+    "LAYOUT_KN", "LAYOUT_NK", "KERNEL_AUTO", "KERNEL_GEMV", "KERNEL_TILED", "KERNEL_GENERIC", "KERNEL_STREAM",
 )
 
 __all__ = list(_KERNEL_NAMES)

@@ -27,7 +27,7 @@ except ImportError as e:  # pragma: no cover - exercised only without a build
 LAYOUT_KN = "kn"  # B [K/2, N], S [K/32, N]  (reference API layout)
 LAYOUT_NK = "nk"  # B [N, K/2], S [N, K/32]  (K-contiguous weights)
 
-KERNEL_AUTO, KERNEL_GEMV, KERNEL_TILED, KERNEL_GENERIC = 0, 1, 2, 3
+KERNEL_AUTO, KERNEL_GEMV, KERNEL_TILED, KERNEL_GENERIC, KERNEL_STREAM = 0, 1, 2, 3, 4
 
 
 def device_info(dev_id=0):

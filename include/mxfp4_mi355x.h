@@ -41,7 +41,8 @@ enum {
   MXFP4_KERNEL_AUTO = 0,    /* cost-model choice */
   MXFP4_KERNEL_GEMV = 1,    /* memory-bound family, M <= 32 */
   MXFP4_KERNEL_TILED = 2,   /* MFMA-bound tiled family */
-  MXFP4_KERNEL_GENERIC = 3  /* one thread per output, any N */
+  MXFP4_KERNEL_GENERIC = 3, /* one thread per output, any N */
+  MXFP4_KERNEL_STREAM = 4   /* split-K weight streaming, M <= 32, [N,K/2], K % 256 == 0 */
 };
 
 /* A launch plan: which kernel family, which tile variant, how many K splits. */

@@ -72,9 +72,25 @@ def _plan(lib, M, N, K, layout=0):
 ])
 def test_every_baseline_shape_has_a_native_plan(lib, M, N, K, layout):
     p, desc = _plan(lib, M, N, K, layout)
-    assert p.kernel in (1, 2), desc  # GEMV family for M <= 32, tiled otherwise
-    assert (p.kernel == 1) == (M <= 32), desc
+    # memory-bound families (GEMV, or streaming for [N,K/2]) for M <= 32, tiled otherwise
+    assert p.kernel in (1, 2, 4), desc
+    assert (p.kernel in (1, 4)) == (M <= 32), desc
+    if p.kernel == 4:
+        assert layout == 1 and K % 256 == 0, desc
     assert p.split_k >= 1
+
+
+def test_stream_plan_validation(lib):
+    ws = lib.mxfp4_gemm_workspace_bytes
+    # split count is fixed by the shape: K / 2048 for variant 0
+    assert ws(16, 8192, 8192, 1, ctypes.byref(Plan(4, 0, 4, 0))) > 0
+    assert ws(16, 8192, 8192, 1, ctypes.byref(Plan(4, 0, 3, 0))) == 0   # wrong split
+    assert ws(16, 8192, 8192, 0, ctypes.byref(Plan(4, 0, 4, 0))) == 0   # [K/2,N] not supported
+    assert ws(17, 8192, 8192, 1, ctypes.byref(Plan(4, 0, 4, 0))) == 0   # M > 16 for mt1
+    assert ws(16, 8192, 8160, 1, ctypes.byref(Plan(4, 0, 4, 0))) == 0   # K % 256 != 0
+    assert ws(16, 8192, 16384, 1, ctypes.byref(Plan(4, 0, 8, 0))) == 0  # more splits than the kernel holds
+    assert ws(32, 8192, 8192, 1, ctypes.byref(Plan(4, 2, 8, 0))) > 0
+    assert ws(16, 8192, 2048, 1, ctypes.byref(Plan(4, 0, 1, 0))) == 0   # one split: no workspace
 
 
 def test_odd_n_goes_generic_for_kn(lib):
@@ -168,8 +184,10 @@ def test_extension_rejects_cpu_tensors_like_reference(kk):
 def test_plan_from_python(kk):
     kind, variant, split, desc = kk.select_plan(4096, 12288, 3072)
     assert kind == 2 and desc.startswith("tiled")
-    kind, _, _, desc = kk.select_plan(16, 8192, 8192, "nk")
-    assert kind == 1 and desc.startswith("gemv")
+    kind, _, split, desc = kk.select_plan(16, 8192, 8192, "nk")
+    assert kind == kk.KERNEL_STREAM and desc.startswith("stream") and split == 2
+    kind, _, _, desc = kk.select_plan(16, 8192, 8192, "kn")
+    assert kind == kk.KERNEL_GEMV and desc.startswith("gemv")
 
 
 def test_product_package_never_imports_oracle():

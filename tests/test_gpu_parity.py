@@ -169,6 +169,58 @@ def test_every_gemv_variant_and_split(kk, layout, M):
     assert ran >= 6
 
 
+# (variant, rows it covers, K per split, K per wave)
+STREAM_VARIANTS = [(0, 16, 2048, 256), (1, 16, 1024, 256), (2, 32, 1024, 256),
+                   (3, 16, 4096, 512), (4, 32, 2048, 512)]
+
+
+@pytest.mark.parametrize("variant,mmax,kr,kw", STREAM_VARIANTS)
+def test_stream_variants(kk, variant, mmax, kr, kw):
+    """Streaming split-K kernel ([N,K/2], M <= 32): ragged M / N, one split,
+    a partial last split (K = kr + kw) and the largest split count (K = 8192)."""
+    import torch
+
+    for M in (1, 7, mmax):
+        for N, K in ((512, min(kr, 2048)), (1000, kr + kw), (4096, 8192), (96, kw)):
+            splits = -(-K // kr)
+            log(f"case stream variant={variant} M={M} N={N} K={K} splits={splits}")
+            A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=M + N + K)
+            ref = oracle_f64(A_bits, W, S)
+            for dt in (torch.float32, torch.bfloat16):
+                out = run_gemm(kk, A_bits, W, S, "nk", dt, plan=(kk.KERNEL_STREAM, variant, splits))
+                bad = mo.strict_violations(out, ref, K)
+                assert bad == 0, f"M={M} N={N} K={K} {dt}: {bad} bad"
+
+
+def test_stream_rejects_unsupported(kk):
+    import torch
+
+    A_bits, W, S = mo.make_inputs(17, 512, 2048, 120, 132, seed=3)
+    with pytest.raises(RuntimeError, match="invalid argument"):  # M > 16 for a 16-row variant
+        run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=(kk.KERNEL_STREAM, 0, 1))
+    with pytest.raises(RuntimeError, match="invalid argument"):  # [K/2,N] weights
+        run_gemm(kk, A_bits[:16], W, S, "kn", torch.float32, plan=(kk.KERNEL_STREAM, 0, 1))
+
+
+def test_stream_repeat_and_shared_workspace(kk):
+    """Counters and packets return to zero after every call: repeated calls are
+    bitwise identical, also when other split-K kernels use the same
+    workspace in between."""
+    import torch
+
+    A16, W16, S16 = mo.make_inputs(16, 8192, 8192, 122, 130, seed=9)
+    ref = oracle_f64(A16, W16, S16)
+    first = run_gemm(kk, A16, W16, S16, "nk", torch.float32)
+    assert mo.strict_violations(first, ref, 8192) == 0
+    assert kk.select_plan(16, 8192, 8192, "nk")[0] == kk.KERNEL_STREAM
+    Am, Wm, Sm = mo.make_inputs(300, 512, 672, 118, 134, seed=2)
+    for i in range(3):
+        again = run_gemm(kk, A16, W16, S16, "nk", torch.float32)
+        assert np.array_equal(first, again), f"repeat {i}"
+        run_gemm(kk, Am, Wm, Sm, "kn", torch.float32, plan=(kk.KERNEL_TILED, 6, 3))
+        run_gemm(kk, A16, W16, S16, "kn", torch.float32, plan=(kk.KERNEL_GEMV, 0, 4))
+
+
 def test_split_k_is_deterministic(kk):
     import torch
 
