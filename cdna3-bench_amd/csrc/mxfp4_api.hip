@@ -89,7 +89,7 @@ int64_t stream_ctas(const StreamShape& s, int64_t N, int64_t K) {
   return ceil_div(ceil_div(N, 32), splits) * splits;
 }
 bool stream_plan_ok(int layout, int64_t M, int64_t N, int64_t K, const StreamShape& s) {
-  if (layout != kLayoutNK || M > 16 * s.mt || K % s.kw != 0) return false;
+  if ((layout != kLayoutNK && layout != kLayoutP) || M > 16 * s.mt || K % s.kw != 0) return false;
   const int64_t splits = stream_splits(s, K);
   if (splits > s.smax) return false;
   if (splits > 1 && stream_ctas(s, N, K) * 4 > (int64_t)MXFP4_COUNTER_BYTES) return false;
@@ -102,10 +102,13 @@ int gemv_steps(int layout, int64_t K) { return (int)(layout == kLayoutKN ? K / 3
 int64_t gemv_tile(const GemvShape& g) { return 16LL * g.mt * 16 * g.cb; }
 
 bool gemv_plan_ok(int layout, int64_t M, int64_t N, const GemvShape& g) {
+  if (layout != kLayoutKN && layout != kLayoutNK) return false;
   if (M > 16 * g.mt) return false;
   if (layout == kLayoutKN && (N % 16 != 0 || g.cb < 4)) return false;
   return gemv_shape_available(layout, g);
 }
+
+void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out);
 
 // Memory-bound family.  [N,K/2]: 32 columns x the whole K per CTA of 16
 // waves (no split needed once N >= 8192).  [K/2,N]: 128 columns per CTA and
@@ -117,7 +120,7 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
   // kernel, first choice that fits (measured on MI355X at N = 8192 / 28672,
   // K = 8192: 512-K waves with 2 splits beat 256-K waves with 4; both beat
   // this family by 1.3-1.7x).
-  if (layout == kLayoutNK) {
+  if (layout == kLayoutNK || layout == kLayoutP) {
     static const int kPrefer16[] = {3, 0, 1}, kPrefer32[] = {4, 2};
     const int* pref = two ? kPrefer32 : kPrefer16;
     const int npref = two ? 2 : 3;
@@ -128,6 +131,12 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
         return;
       }
     }
+  }
+  if (layout != kLayoutKN && layout != kLayoutNK) {
+    // prepacked layouts the streaming kernel does not take: the pipelined
+    // tiled kernel with split-K
+    choose_tiled(layout, M, N, K, out);
+    return;
   }
   int want;
   if (layout == kLayoutKN)
@@ -145,6 +154,21 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
   out->reserved = 0;
 }
 
+// The G loader uses the [K/2,N] lane map and the panel loader the [N,K/2]
+// one (mxfp4_tiled_pipe.hip).
+double tiled_eff(const TiledVariant& v, int layout) {
+  return layout == kLayoutKN || layout == kLayoutG ? v.eff_kn : v.eff_nk;
+}
+
+// Tiled variants a layout may use: the prepacked layouts only have loaders
+// in the pipelined kernel, whose [N,K/2] loader reads aligned scale dwords.
+bool tiled_variant_ok(const TiledVariant& v, int layout, int64_t K) {
+  if (!v.pipe) return layout == kLayoutKN || layout == kLayoutNK;
+  if (layout == kLayoutNK) return K % 128 == 0;
+  if (layout == kLayoutG) return v.shape.bn() % kGCols == 0;
+  return true;
+}
+
 double tiled_time(const TiledVariant& v, int layout, int64_t M, int64_t N, int64_t K, int splits) {
   const int bm = v.shape.bm(), bn = v.shape.bn();
   const int64_t tiles = ceil_div(M, bm) * ceil_div(N, bn);
@@ -153,7 +177,7 @@ double tiled_time(const TiledVariant& v, int layout, int64_t M, int64_t N, int64
   const int64_t ctas = tiles * ceil_div(ksteps, per_split);
   const double slots = kNumCus * v.ctas_per_cu;
   const double rounds = std::ceil((double)ctas / slots);
-  const double cu_rate = kMfmaFlopsPerS / kNumCus * (layout == kLayoutKN ? v.eff_kn : v.eff_nk);
+  const double cu_rate = kMfmaFlopsPerS / kNumCus * tiled_eff(v, layout);
   const double t_cta = (double)bm * bn * per_split * 64 * 2.0 * v.ctas_per_cu / cu_rate;
   double t = rounds * t_cta;
   const double t_hbm = problem_bytes(M, N, K, 2) / kHbmBytesPerS;
@@ -170,7 +194,7 @@ void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) 
   const int64_t ksteps = ceil_div(K, 64);
   for (int v = 0; v < kNumTiled; ++v) {
     const TiledVariant& tv = kTiled[v];
-    if (tv.pipe && layout == kLayoutNK && K % 128 != 0) continue;
+    if (!tiled_variant_ok(tv, layout, K)) continue;
     const int64_t tiles = ceil_div(M, tv.shape.bm()) * ceil_div(N, tv.shape.bn());
     for (int s = 1; s <= 16 && s <= ksteps; ++s) {
       if (s > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) break;
@@ -212,8 +236,7 @@ hipError_t validate_plan(int layout, int64_t M, int64_t N, int64_t K, const mxfp
     case MXFP4_KERNEL_TILED: {
       if (p.variant < 0 || p.variant >= kNumTiled) return hipErrorInvalidValue;
       if (layout == kLayoutKN && N % 16 != 0) return hipErrorInvalidValue;
-      // the pipelined kernel reads [N,K/2] scales as aligned dwords of 4 groups
-      if (kTiled[p.variant].pipe && layout == kLayoutNK && K % 128 != 0) return hipErrorInvalidValue;
+      if (!tiled_variant_ok(kTiled[p.variant], layout, K)) return hipErrorInvalidValue;
       const TiledShape& s = kTiled[p.variant].shape;
       const int64_t tiles = ceil_div(M, s.bm()) * ceil_div(N, s.bn());
       if (p.split_k > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) return hipErrorInvalidValue;
@@ -259,12 +282,16 @@ size_t plan_workspace(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_p
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+bool layout_ok(int layout, int64_t N, int64_t K) {
+  return layout >= kLayoutKN && layout <= kLayoutP && layout_shape_ok(layout, N, K);
+}
+
 hipError_t check_args(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype,
                       int64_t M, int64_t N, int64_t K, int layout) {
   if (M < 0 || N < 0 || K < 0) return hipErrorInvalidValue;
   if (K % 32 != 0) return hipErrorInvalidValue;
   if (M > INT32_MAX || N > INT32_MAX || K > (1LL << 21)) return hipErrorInvalidValue;
-  if (layout != kLayoutKN && layout != kLayoutNK) return hipErrorInvalidValue;
+  if (!layout_ok(layout, N, K)) return hipErrorInvalidValue;
   if (c_dtype != MXFP4_OUT_F32 && c_dtype != MXFP4_OUT_BF16) return hipErrorInvalidValue;
   if (M * N == 0) return hipSuccess;
   if (!C) return hipErrorInvalidValue;
@@ -333,7 +360,7 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
       a.partials = a.splits > 1 ? partials : nullptr;
       a.counters = a.splits > 1 ? counters : nullptr;
       a.spin_limit = kStreamSpin;
-      return launch_stream(s, a, stream);
+      return launch_stream(layout, s, a, stream);
     }
     case MXFP4_KERNEL_TILED: {
       const TiledShape& s = kTiled[plan.variant].shape;
@@ -366,7 +393,7 @@ extern "C" {
 
 hipError_t mxfp4_select_plan(int64_t M, int64_t N, int64_t K, int b_layout, mxfp4_plan* out) {
   if (!out || M < 0 || N < 0 || K < 0 || K % 32 != 0) return hipErrorInvalidValue;
-  if (b_layout != kLayoutKN && b_layout != kLayoutNK) return hipErrorInvalidValue;
+  if (!layout_ok(b_layout, N, K)) return hipErrorInvalidValue;
   auto_plan(b_layout, M, N, K, out);
   return hipSuccess;
 }
@@ -408,7 +435,7 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
 size_t mxfp4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int b_layout,
                                   const mxfp4_plan* plan) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 32 != 0) return 0;
-  if (b_layout != kLayoutKN && b_layout != kLayoutNK) return 0;
+  if (!layout_ok(b_layout, N, K)) return 0;
   mxfp4_plan p;
   if (plan && plan->kernel != MXFP4_KERNEL_AUTO) {
     p = *plan;
@@ -436,10 +463,26 @@ hipError_t mxfp4_dequant(const uint8_t* B, const uint8_t* S, void* out, int out_
                          int64_t N, int b_layout, hipStream_t stream) {
   if (K < 0 || N < 0 || K % 32 != 0 || K > INT32_MAX || N > INT32_MAX) return hipErrorInvalidValue;
   if (out_dtype != MXFP4_OUT_F32 && out_dtype != MXFP4_OUT_BF16) return hipErrorInvalidValue;
-  if (b_layout != kLayoutKN && b_layout != kLayoutNK) return hipErrorInvalidValue;
+  if (!layout_ok(b_layout, N, K)) return hipErrorInvalidValue;
   if (K * N == 0) return hipSuccess;
   if (!B || !S || !out) return hipErrorInvalidValue;
   return launch_dequant(b_layout, B, S, out, out_dtype == MXFP4_OUT_BF16, (int)K, (int)N, stream);
+}
+
+hipError_t mxfp4_convert_layout(const uint8_t* B, const uint8_t* S, int src_layout, uint8_t* B_out,
+                                uint8_t* S_out, int dst_layout, int64_t K, int64_t N,
+                                hipStream_t stream) {
+  if (K < 0 || N < 0 || K % 32 != 0) return hipErrorInvalidValue;
+  if (!layout_ok(src_layout, N, K) || !layout_ok(dst_layout, N, K)) return hipErrorInvalidValue;
+  if (K * N == 0) return hipSuccess;
+  if (!B || !S || !B_out || !S_out || !aligned16(B_out)) return hipErrorInvalidValue;
+  // one thread per 16 code bytes / per scale byte, 256 per block
+  if ((uint64_t)(K / 32) * (uint64_t)N / 256 >= (1ull << 31)) return hipErrorInvalidValue;
+  const uint64_t code_bytes = (uint64_t)K / 2 * N, scale_bytes = (uint64_t)K / 32 * N;
+  const uint64_t b0 = (uintptr_t)B, b1 = b0 + code_bytes, o0 = (uintptr_t)B_out, o1 = o0 + code_bytes;
+  const uint64_t s0 = (uintptr_t)S, s1 = s0 + scale_bytes, t0 = (uintptr_t)S_out, t1 = t0 + scale_bytes;
+  if ((b0 < o1 && o0 < b1) || (s0 < t1 && t0 < s1)) return hipErrorInvalidValue;  // overlap
+  return launch_convert(src_layout, dst_layout, B, S, B_out, S_out, (size_t)K, (size_t)N, stream);
 }
 
 int mxfp4_shape_supported(char strategy, int64_t M, int64_t N, int64_t K) {

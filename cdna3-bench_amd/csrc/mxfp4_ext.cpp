@@ -9,9 +9,11 @@
 // Every letter keeps the reference's accepted shapes (strategy A/B reject
 // shapes outside shape_supported_c with "launch_strategy_x: invalid argument",
 // the others raise "Strategy X requires ..."), and all of them run the one
-// gfx950 path chosen by the library's cost model.  Additions: gemm_auto
-// (every shape with K % 32 == 0), gemm (either weight layout, explicit plan),
-// dequant, select_plan.  C may be fp32 (the reference's only dtype) or bf16.
+// gfx950 path chosen by the library's cost model; gemm_g reads the G
+// prepack directly.  Additions: gemm_auto (every shape with K % 32 == 0),
+// gemm (any weight layout, explicit plan), dequant, convert_layout (device
+// prepack between layouts), select_plan.  C may be fp32 (the reference's
+// only dtype) or bf16.
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
 
@@ -42,6 +44,18 @@ torch::Tensor workspace_for(const torch::Tensor& like, size_t bytes) {
   return it->second;
 }
 
+// Layout names of the Python API.
+int layout_code(const std::string& layout) {
+  if (layout == "kn") return MXFP4_LAYOUT_KN;
+  if (layout == "nk") return MXFP4_LAYOUT_NK;
+  if (layout == "g") return MXFP4_LAYOUT_G;
+  if (layout == "p") return MXFP4_LAYOUT_P;
+  TORCH_CHECK(false, "layout must be 'kn', 'nk', 'g' or 'p'");
+  return -1;
+}
+
+bool prepacked(int layout) { return layout == MXFP4_LAYOUT_G || layout == MXFP4_LAYOUT_P; }
+
 int out_code(const torch::Tensor& C) {
   return C.scalar_type() == at::kBFloat16 ? MXFP4_OUT_BF16 : MXFP4_OUT_F32;
 }
@@ -60,6 +74,10 @@ hipStream_t check_inputs(const torch::Tensor& A, const torch::Tensor& B, const t
   if (layout == MXFP4_LAYOUT_KN) {
     TORCH_CHECK(B.dim() == 2 && B.size(0) == K / 2 && B.size(1) == N, "B_packed shape");
     TORCH_CHECK(S.dim() == 2 && S.size(0) == K / 32 && S.size(1) == N, "B_scales shape");
+  } else if (prepacked(layout)) {
+    // any shape with the layout's element count (the reference passes flat arrays)
+    TORCH_CHECK(B.numel() == K / 2 * N, "B_packed size");
+    TORCH_CHECK(S.numel() == K / 32 * N, "B_scales size");
   } else {
     TORCH_CHECK(B.dim() == 2 && B.size(0) == N && B.size(1) == K / 2, "B_packed shape");
     TORCH_CHECK(S.dim() == 2 && S.size(0) == N && S.size(1) == K / 32, "B_scales shape");
@@ -142,15 +160,24 @@ torch::Tensor gemm_auto(const torch::Tensor& A, const torch::Tensor& B, const to
   return dispatch("gemm_auto", A, B, S, C);
 }
 
-// Either weight layout ("kn": [K/2,N]/[K/32,N], "nk": [N,K/2]/[N,K/32]),
-// output dtype, and an optional explicit plan (kernel, variant, split_k).
+// Any weight layout ("kn": [K/2,N]/[K/32,N], "nk": [N,K/2]/[N,K/32], "g":
+// the strategy-G prepack, "p": panels; g and p in any shape of the right
+// size, N = numel / (K/2)), output dtype, and an optional explicit plan
+// (kernel, variant, split_k).
 torch::Tensor gemm(const torch::Tensor& A, const torch::Tensor& B, const torch::Tensor& S,
                    c10::optional<torch::Tensor> C_opt, const std::string& layout,
                    c10::optional<at::ScalarType> out_dtype, c10::optional<std::vector<int64_t>> plan) {
-  TORCH_CHECK(layout == "kn" || layout == "nk", "layout must be 'kn' or 'nk'");
-  const int lay = layout == "kn" ? MXFP4_LAYOUT_KN : MXFP4_LAYOUT_NK;
-  TORCH_CHECK(A.dim() == 2 && B.dim() == 2, "A shape");
-  const int64_t M = A.size(0), K = A.size(1), N = lay == MXFP4_LAYOUT_KN ? B.size(1) : B.size(0);
+  const int lay = layout_code(layout);
+  TORCH_CHECK(A.dim() == 2 && (prepacked(lay) || B.dim() == 2), "A shape");
+  const int64_t M = A.size(0), K = A.size(1);
+  TORCH_CHECK(K % 32 == 0, "K must be a multiple of 32");
+  int64_t N;
+  if (lay == MXFP4_LAYOUT_KN)
+    N = B.size(1);
+  else if (lay == MXFP4_LAYOUT_NK)
+    N = B.size(0);
+  else
+    N = K == 0 ? 0 : B.numel() / (K / 2);
   at::ScalarType dt = out_dtype.has_value() ? *out_dtype : at::kFloat;
   torch::Tensor C = C_opt.has_value() ? *C_opt : torch::empty({M, N}, A.options().dtype(dt));
   auto stream = check_inputs(A, B, S, C, M, N, K, lay);
@@ -185,36 +212,108 @@ torch::Tensor gemm_g(const torch::Tensor& A, const torch::Tensor& B_prep,
   TORCH_CHECK((C.scalar_type() == at::kFloat || C.scalar_type() == at::kBFloat16) && C.dim() == 2 &&
                   C.size(0) == M && C.size(1) == N && C.is_contiguous(),
               "C shape/contig");
-  TORCH_CHECK(false, "gemm_g: prepacked layout not available in this build");
+  TORCH_CHECK(A.get_device() == B_prep.get_device() && A.get_device() == Bs_prep.get_device() &&
+                  A.get_device() == C.get_device(),
+              "all tensors must be on the same GPU");
+  auto stream = c10::hip::getCurrentHIPStream(A.get_device()).stream();
+  launch("launch_strategy_g", A, B_prep, Bs_prep, C, M, N, K, MXFP4_LAYOUT_G, nullptr, stream);
   return C;
 }
 
+// Shape a layout's code / scale tensors take when this API allocates them.
+std::vector<int64_t> code_shape(int layout, int64_t K, int64_t N) {
+  switch (layout) {
+    case MXFP4_LAYOUT_KN: return {K / 2, N};
+    case MXFP4_LAYOUT_NK: return {N, K / 2};
+    case MXFP4_LAYOUT_G: return {N / 128, K / 8, 128, 4};
+    default: return {N / 32, K / 64, 2, 32, 16};
+  }
+}
+std::vector<int64_t> scale_shape(int layout, int64_t K, int64_t N) {
+  switch (layout) {
+    case MXFP4_LAYOUT_KN: return {K / 32, N};
+    case MXFP4_LAYOUT_NK: return {N, K / 32};
+    case MXFP4_LAYOUT_G: return {N / 128, K / 32, 128};
+    default: return {N / 32, K / 64, 2, 32};
+  }
+}
+
+// (K, N) of weights in `layout`: from the 2-D shapes of kn/nk, from K (given,
+// or the leading dims of the shapes convert_layout returns) for g/p.
+std::pair<int64_t, int64_t> weight_dims(const torch::Tensor& B, int layout, c10::optional<int64_t> K_opt) {
+  if (layout == MXFP4_LAYOUT_KN || layout == MXFP4_LAYOUT_NK) {
+    TORCH_CHECK(B.dim() == 2, "B must be 2-D for layout kn / nk");
+    const bool kn = layout == MXFP4_LAYOUT_KN;
+    return {(kn ? B.size(0) : B.size(1)) * 2, kn ? B.size(1) : B.size(0)};
+  }
+  int64_t K;
+  if (K_opt.has_value()) {
+    K = *K_opt;
+  } else {
+    TORCH_CHECK(B.dim() >= 2, "pass K for flat prepacked weights");
+    K = B.size(1) * (layout == MXFP4_LAYOUT_G ? 8 : 64);
+  }
+  TORCH_CHECK(K > 0 && K % 32 == 0 && B.numel() % (K / 2) == 0, "B size not consistent with K");
+  return {K, B.numel() / (K / 2)};
+}
+
+// Weights rewritten into another layout on the device (prepack / unprepack);
+// returns (codes, scales) shaped for dst (code_shape / scale_shape).
+py::tuple convert_layout(const torch::Tensor& B, const torch::Tensor& S, const std::string& src,
+                         const std::string& dst, c10::optional<int64_t> K_opt) {
+  const int ls = layout_code(src), ld = layout_code(dst);
+  TORCH_CHECK(B.is_cuda() && S.is_cuda(), "all tensors must be on GPU");
+  TORCH_CHECK(B.scalar_type() == at::kByte && S.scalar_type() == at::kByte, "B and S must be uint8");
+  TORCH_CHECK(B.is_contiguous() && S.is_contiguous(), "B/S must be contiguous");
+  TORCH_CHECK(B.get_device() == S.get_device(), "all tensors must be on the same GPU");
+  const auto kn = weight_dims(B, ls, K_opt);
+  const int64_t K = kn.first, N = kn.second;
+  TORCH_CHECK(K % 32 == 0, "K must be a multiple of 32");
+  TORCH_CHECK(S.numel() == K / 32 * N, "B_scales size");
+  TORCH_CHECK((ld != MXFP4_LAYOUT_G && ls != MXFP4_LAYOUT_G) || N % 128 == 0, "layout g needs N % 128 == 0");
+  TORCH_CHECK((ld != MXFP4_LAYOUT_P && ls != MXFP4_LAYOUT_P) || (N % 32 == 0 && K % 64 == 0),
+              "layout p needs N % 32 == 0 and K % 64 == 0");
+  torch::Tensor Bo = torch::empty(code_shape(ld, K, N), B.options());
+  torch::Tensor So = torch::empty(scale_shape(ld, K, N), S.options());
+  auto stream = c10::hip::getCurrentHIPStream(B.get_device()).stream();
+  hipError_t err = mxfp4_convert_layout(static_cast<const uint8_t*>(B.data_ptr()),
+                                        static_cast<const uint8_t*>(S.data_ptr()), ls,
+                                        static_cast<uint8_t*>(Bo.data_ptr()),
+                                        static_cast<uint8_t*>(So.data_ptr()), ld, K, N, stream);
+  TORCH_CHECK(err == hipSuccess, "mxfp4_convert_layout: ", hipGetErrorString(err));
+  return py::make_tuple(Bo, So);
+}
+
 torch::Tensor dequant(const torch::Tensor& B, const torch::Tensor& S, const std::string& layout,
-                      at::ScalarType out_dtype) {
-  TORCH_CHECK(layout == "kn" || layout == "nk", "layout must be 'kn' or 'nk'");
+                      at::ScalarType out_dtype, c10::optional<int64_t> K_opt) {
+  const int lay = layout_code(layout);
   TORCH_CHECK(B.is_cuda() && S.is_cuda(), "all tensors must be on GPU");
   TORCH_CHECK(B.scalar_type() == at::kByte && S.scalar_type() == at::kByte, "B and S must be uint8");
   TORCH_CHECK(out_dtype == at::kFloat || out_dtype == at::kBFloat16, "out_dtype must be float32 or bfloat16");
-  TORCH_CHECK(B.dim() == 2 && S.dim() == 2 && B.is_contiguous() && S.is_contiguous(), "B/S must be 2-D contiguous");
-  const bool kn = layout == "kn";
-  const int64_t K = (kn ? B.size(0) : B.size(1)) * 2, N = kn ? B.size(1) : B.size(0);
+  TORCH_CHECK(B.is_contiguous() && S.is_contiguous(), "B/S must be contiguous");
+  const auto kn_dims = weight_dims(B, lay, K_opt);
+  const int64_t K = kn_dims.first, N = kn_dims.second;
   TORCH_CHECK(K % 32 == 0, "K must be a multiple of 32");
-  TORCH_CHECK(kn ? (S.size(0) == K / 32 && S.size(1) == N) : (S.size(0) == N && S.size(1) == K / 32),
-              "B_scales shape");
+  if (lay == MXFP4_LAYOUT_KN || lay == MXFP4_LAYOUT_NK) {
+    const bool kn = lay == MXFP4_LAYOUT_KN;
+    TORCH_CHECK(S.dim() == 2 && (kn ? (S.size(0) == K / 32 && S.size(1) == N) : (S.size(0) == N && S.size(1) == K / 32)),
+                "B_scales shape");
+  } else {
+    TORCH_CHECK(S.numel() == K / 32 * N, "B_scales size");
+  }
   torch::Tensor out = torch::empty({K, N}, B.options().dtype(out_dtype));
   auto stream = c10::hip::getCurrentHIPStream(B.get_device()).stream();
   hipError_t err = mxfp4_dequant(static_cast<const uint8_t*>(B.data_ptr()),
                                  static_cast<const uint8_t*>(S.data_ptr()), out.data_ptr(),
                                  out_dtype == at::kBFloat16 ? MXFP4_OUT_BF16 : MXFP4_OUT_F32, K, N,
-                                 kn ? MXFP4_LAYOUT_KN : MXFP4_LAYOUT_NK, stream);
+                                 lay, stream);
   TORCH_CHECK(err == hipSuccess, "mxfp4_dequant: ", hipGetErrorString(err));
   return out;
 }
 
 py::tuple select_plan(int64_t M, int64_t N, int64_t K, const std::string& layout) {
-  TORCH_CHECK(layout == "kn" || layout == "nk", "layout must be 'kn' or 'nk'");
   mxfp4_plan p{};
-  hipError_t err = mxfp4_select_plan(M, N, K, layout == "kn" ? MXFP4_LAYOUT_KN : MXFP4_LAYOUT_NK, &p);
+  hipError_t err = mxfp4_select_plan(M, N, K, layout_code(layout), &p);
   TORCH_CHECK(err == hipSuccess, "mxfp4_select_plan: ", hipGetErrorString(err));
   char buf[128];
   mxfp4_plan_describe(&p, buf, sizeof(buf));
@@ -263,7 +362,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gemm", &gemm, py::arg("A"), py::arg("B"), py::arg("S"), py::arg("C") = py::none(),
         py::arg("layout") = "kn", py::arg("out_dtype") = py::none(), py::arg("plan") = py::none());
   m.def("dequant", &dequant, py::arg("B"), py::arg("S"), py::arg("layout") = "kn",
-        py::arg("out_dtype") = at::kBFloat16);
+        py::arg("out_dtype") = at::kBFloat16, py::arg("K") = py::none());
+  m.def("convert_layout", &convert_layout, py::arg("B"), py::arg("S"), py::arg("src"), py::arg("dst"),
+        py::arg("K") = py::none());
   m.def("select_plan", &select_plan, py::arg("M"), py::arg("N"), py::arg("K"), py::arg("layout") = "kn");
   m.def("device_info", &device_info, py::arg("dev_id") = 0);
   m.def("shape_supported_c", [](int64_t M, int64_t N, int64_t K) { return shape_supported('c', M, N, K); },

@@ -6,9 +6,9 @@
 #include <stddef.h>
 #include <stdint.h>
 
-namespace mxfp4 {
+#include "mxfp4_layout.h"
 
-enum Layout : int { kLayoutKN = 0, kLayoutNK = 1 };
+namespace mxfp4 {
 
 // Tiled MFMA family (M > 32): BM x BN x 64 tiles, WM x WN waves, each wave
 // owning RB 32-row blocks x 128 columns, bf16 MFMA 32x32x16.
@@ -74,7 +74,7 @@ hipError_t launch_gemv(int layout, const GemvShape& shape, const GemvArgs& args,
                        hipStream_t stream);
 bool gemv_shape_available(int layout, const GemvShape& shape);
 
-// Streaming split-K family for M <= 32 and [N,K/2] weights (mxfp4_stream.hip):
+// Streaming split-K family for M <= 32 and [N,K/2] or P weights (mxfp4_stream.hip):
 // 32-column groups, K in `splits` ranges of waves * kw, one CTA per
 // (group block, split) processing `splits` units; partials travel as tagged
 // packets.
@@ -104,17 +104,21 @@ struct StreamShape {
   int tile() const { return 16 * mt * 16 * gcb; }
 };
 
-hipError_t launch_stream(const StreamShape& shape, const StreamArgs& args, hipStream_t stream);
+hipError_t launch_stream(int layout, const StreamShape& shape, const StreamArgs& args, hipStream_t stream);
 bool stream_shape_available(const StreamShape& shape);
 
 // Any shape with K % 32 == 0; one thread per output, for shapes the fast
-// families do not cover (N % 16 != 0).
+// families do not cover (N % 16 != 0, unaligned pointers).
 hipError_t launch_generic(int layout, const uint16_t* A, const uint8_t* B, const uint8_t* S,
                           void* C, int out_bf16, int M, int N, int K, hipStream_t stream);
 
 // Dequantized [K, N] tile (bf16 or fp32) from either layout.
 hipError_t launch_dequant(int layout, const uint8_t* B, const uint8_t* S, void* out,
                           int out_bf16, int K, int N, hipStream_t stream);
+
+// Weights rewritten from one layout to another (codes and scales).
+hipError_t launch_convert(int src_layout, int dst_layout, const uint8_t* B, const uint8_t* S,
+                          uint8_t* B_out, uint8_t* S_out, size_t K, size_t N, hipStream_t stream);
 
 // C = 0 (K == 0).
 hipError_t launch_zero_fill(void* C, size_t bytes, hipStream_t stream);

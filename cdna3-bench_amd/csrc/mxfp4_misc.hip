@@ -1,17 +1,22 @@
-// Dequant tile, generic fallback GEMM and zero fill.
+// Dequant tile, generic fallback GEMM, weight layout conversion and zero fill.
 //
 // dequant_kernel replaces the reference's dequant-only pass
 // (csrc/strategy_a_two_pass.cu:8-37, which writes a bf16 [K, N] scratch) and
 // is the device counterpart of ref.py:50-72 (dequantize_mxfp4, axis=0).  It
 // uses the same v_cvt_scalef32_pk_bf16_fp4 convert as the GEMM kernels, so
 // the bit-exact tile test pins the GEMM's in-register dequant as well.
+//
+// convert_*_kernel is the device counterpart of prepack_b_mxfp4
+// (python/mxfp4_cdna3/ref.py:85-101), generalised to any pair of layouts.
 #include "mxfp4_device.h"
 #include "mxfp4_kernels.h"
 
 namespace mxfp4 {
 namespace {
 
-// One thread per packed byte (two K-adjacent codes of one column).
+// One thread per packed byte (two K-adjacent codes of one column), in
+// [K/2, N] order so the writes stay coalesced; the source positions follow
+// the weight layout (mxfp4_layout.h).
 template <int LAYOUT>
 __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict__ B,
                                                       const uint8_t* __restrict__ S, void* out,
@@ -19,20 +24,9 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict_
   const size_t total = (size_t)(K / 2) * N;
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total) return;
-  size_t r, n;
-  uint32_t byte, sbyte;
-  if constexpr (LAYOUT == kLayoutKN) {
-    r = idx / N;
-    n = idx - r * N;
-    byte = B[idx];
-    sbyte = S[(r / 16) * N + n];
-  } else {
-    // Thread order follows [K/2, N] so the writes below stay coalesced.
-    r = idx / N;
-    n = idx - r * N;
-    byte = B[n * (size_t)(K / 2) + r];
-    sbyte = S[n * (size_t)(K / 32) + r / 16];
-  }
+  const size_t r = idx / N, n = idx - r * N;
+  const uint32_t byte = B[code_offset<LAYOUT>(r, n, K, N)];
+  const uint32_t sbyte = S[scale_offset<LAYOUT>(r / 16, n, K, N)];
   const uint32_t v = fp4x2_to_bf16x2<0>(byte, e8m0_to_f32(sbyte));
   const size_t o0 = (2 * r) * (size_t)N + n, o1 = o0 + N;
   if (out_bf16) {
@@ -55,14 +49,8 @@ __global__ void __launch_bounds__(256) generic_kernel(const uint16_t* __restrict
   const int m = (int)(idx / N), n = (int)(idx - (size_t)m * N);
   float acc = 0.f;
   for (int kp = 0; kp < K / 2; ++kp) {
-    uint32_t byte, sbyte;
-    if constexpr (LAYOUT == kLayoutKN) {
-      byte = B[(size_t)kp * N + n];
-      sbyte = S[(size_t)(kp / 16) * N + n];
-    } else {
-      byte = B[(size_t)n * (K / 2) + kp];
-      sbyte = S[(size_t)n * (K / 32) + kp / 16];
-    }
+    const uint32_t byte = B[code_offset<LAYOUT>(kp, n, K, N)];
+    const uint32_t sbyte = S[scale_offset<LAYOUT>(kp / 16, n, K, N)];
     const uint32_t w = fp4x2_to_bf16x2<0>(byte, e8m0_to_f32(sbyte));
     const float a0 = __builtin_bit_cast(float, (uint32_t)A[(size_t)m * K + 2 * kp] << 16);
     const float a1 = __builtin_bit_cast(float, (uint32_t)A[(size_t)m * K + 2 * kp + 1] << 16);
@@ -73,6 +61,64 @@ __global__ void __launch_bounds__(256) generic_kernel(const uint16_t* __restrict
     static_cast<uint16_t*>(C)[idx] = (uint16_t)bf16_bits_rne(acc);
   else
     static_cast<float*>(C)[idx] = acc;
+}
+
+// Layout conversion of the codes: one thread per 16 destination bytes (one
+// 16-byte store).  The 16 bytes' positions (kp, n) follow from the first one
+// in every destination layout except [K/2, N] with N % 16 != 0, where the
+// row may end inside the vector.  Sources whose 16 bytes are one aligned
+// vector as well ([N,K/2] <-> panels) are read as one 16-byte load.
+template <int SRC, int DST>
+__global__ void __launch_bounds__(256) convert_codes_kernel(const uint8_t* __restrict__ B,
+                                                            uint8_t* __restrict__ out, size_t K,
+                                                            size_t N) {
+  const size_t total = K / 2 * N;
+  const size_t o = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
+  if (o >= total) return;
+  size_t kp0, n0;
+  code_position<DST>(o, K, N, kp0, n0);
+  constexpr bool kRun = DST == kLayoutNK || DST == kLayoutP;  // 16 consecutive kp of one column
+  if constexpr (kRun && (SRC == kLayoutNK || SRC == kLayoutP)) {
+    *reinterpret_cast<u32x4*>(out + o) =
+        *reinterpret_cast<const u32x4*>(B + code_offset<SRC>(kp0, n0, K, N));
+    return;
+  }
+  uint8_t v[16];
+  const bool kn_row = DST == kLayoutKN && N % 16 == 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    size_t kp = kp0, n = n0;
+    if constexpr (kRun) {
+      kp = kp0 + i;
+    } else if constexpr (DST == kLayoutG) {
+      kp = kp0 + i % 4;
+      n = n0 + i / 4;
+    } else {
+      if (kn_row)
+        n = n0 + i;
+      else
+        code_position<DST>(o + i, K, N, kp, n);
+    }
+    v[i] = B[code_offset<SRC>(kp, n, K, N)];
+  }
+  u32x4 w;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    w[j] = (uint32_t)v[4 * j] | ((uint32_t)v[4 * j + 1] << 8) | ((uint32_t)v[4 * j + 2] << 16) |
+           ((uint32_t)v[4 * j + 3] << 24);
+  *reinterpret_cast<u32x4*>(out + o) = w;
+}
+
+// Layout conversion of the scales: one thread per destination byte.
+template <int SRC, int DST>
+__global__ void __launch_bounds__(256) convert_scales_kernel(const uint8_t* __restrict__ S,
+                                                             uint8_t* __restrict__ out, size_t K,
+                                                             size_t N) {
+  const size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= K / 32 * N) return;
+  size_t g, n;
+  scale_position<DST>(o, K, N, g, n);
+  out[o] = S[scale_offset<SRC>(g, n, K, N)];
 }
 
 __global__ void __launch_bounds__(256) zero_fill_kernel(uint8_t* p, size_t bytes) {
@@ -86,32 +132,85 @@ __global__ void __launch_bounds__(256) zero_fill_kernel(uint8_t* p, size_t bytes
 
 }  // namespace
 
+namespace {
+
+template <template <int> class F, typename... Args>
+hipError_t by_layout(int layout, Args... args) {
+  switch (layout) {
+    case kLayoutKN: return F<kLayoutKN>::run(args...);
+    case kLayoutNK: return F<kLayoutNK>::run(args...);
+    case kLayoutG: return F<kLayoutG>::run(args...);
+    case kLayoutP: return F<kLayoutP>::run(args...);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int L>
+struct DequantLaunch {
+  static hipError_t run(const uint8_t* B, const uint8_t* S, void* out, int out_bf16, int K, int N,
+                        hipStream_t stream) {
+    const size_t total = (size_t)(K / 2) * N;
+    hipLaunchKernelGGL(dequant_kernel<L>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       B, S, out, out_bf16, K, N);
+    return hipGetLastError();
+  }
+};
+
+template <int L>
+struct GenericLaunch {
+  static hipError_t run(const uint16_t* A, const uint8_t* B, const uint8_t* S, void* C, int out_bf16,
+                        int M, int N, int K, hipStream_t stream) {
+    const size_t total = (size_t)M * N;
+    hipLaunchKernelGGL(generic_kernel<L>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       A, B, S, C, out_bf16, M, N, K);
+    return hipGetLastError();
+  }
+};
+
+template <int SRC>
+struct ConvertFrom {
+  template <int DST>
+  struct To {
+    static hipError_t run(const uint8_t* B, const uint8_t* S, uint8_t* B_out, uint8_t* S_out,
+                          size_t K, size_t N, hipStream_t stream) {
+      const size_t vecs = K / 2 * N / 16, sbytes = K / 32 * N;
+      hipLaunchKernelGGL((convert_codes_kernel<SRC, DST>), dim3((unsigned)((vecs + 255) / 256)),
+                         dim3(256), 0, stream, B, B_out, K, N);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((convert_scales_kernel<SRC, DST>), dim3((unsigned)((sbytes + 255) / 256)),
+                         dim3(256), 0, stream, S, S_out, K, N);
+      return hipGetLastError();
+    }
+  };
+};
+
+template <int SRC>
+struct ConvertLaunch {
+  static hipError_t run(int dst, const uint8_t* B, const uint8_t* S, uint8_t* B_out, uint8_t* S_out,
+                        size_t K, size_t N, hipStream_t stream) {
+    return by_layout<ConvertFrom<SRC>::template To>(dst, B, S, B_out, S_out, K, N, stream);
+  }
+};
+
+}  // namespace
+
 hipError_t launch_dequant(int layout, const uint8_t* B, const uint8_t* S, void* out, int out_bf16,
                           int K, int N, hipStream_t stream) {
-  const size_t total = (size_t)(K / 2) * N;
-  if (total == 0) return hipSuccess;
-  const dim3 grid((unsigned)((total + 255) / 256));
-  if (layout == kLayoutKN)
-    hipLaunchKernelGGL(dequant_kernel<kLayoutKN>, grid, dim3(256), 0, stream, B, S, out, out_bf16, K, N);
-  else if (layout == kLayoutNK)
-    hipLaunchKernelGGL(dequant_kernel<kLayoutNK>, grid, dim3(256), 0, stream, B, S, out, out_bf16, K, N);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  if ((size_t)(K / 2) * N == 0) return hipSuccess;
+  return by_layout<DequantLaunch>(layout, B, S, out, out_bf16, K, N, stream);
 }
 
 hipError_t launch_generic(int layout, const uint16_t* A, const uint8_t* B, const uint8_t* S,
                           void* C, int out_bf16, int M, int N, int K, hipStream_t stream) {
-  const size_t total = (size_t)M * N;
-  if (total == 0) return hipSuccess;
-  const dim3 grid((unsigned)((total + 255) / 256));
-  if (layout == kLayoutKN)
-    hipLaunchKernelGGL(generic_kernel<kLayoutKN>, grid, dim3(256), 0, stream, A, B, S, C, out_bf16, M, N, K);
-  else if (layout == kLayoutNK)
-    hipLaunchKernelGGL(generic_kernel<kLayoutNK>, grid, dim3(256), 0, stream, A, B, S, C, out_bf16, M, N, K);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  if ((size_t)M * N == 0) return hipSuccess;
+  return by_layout<GenericLaunch>(layout, A, B, S, C, out_bf16, M, N, K, stream);
+}
+
+hipError_t launch_convert(int src_layout, int dst_layout, const uint8_t* B, const uint8_t* S,
+                          uint8_t* B_out, uint8_t* S_out, size_t K, size_t N, hipStream_t stream) {
+  if (K * N == 0) return hipSuccess;
+  return by_layout<ConvertLaunch>(src_layout, dst_layout, B, S, B_out, S_out, K, N, stream);
 }
 
 hipError_t launch_zero_fill(void* C, size_t bytes, hipStream_t stream) {

@@ -1,4 +1,5 @@
-// Streaming split-K kernel for M <= 32 with [N, K/2] weights (decode shapes).
+// Streaming split-K kernel for M <= 32 with [N, K/2] or panel (P) weights
+// (decode shapes).
 //
 // The reference has no kernel for these shapes (every launcher rejects
 // M % 64 != 0, csrc/common.h:80-99).  Design points, all measured on MI355X:
@@ -15,6 +16,11 @@
 //   are S times fewer than with whole-K CTAs.
 // * Scales: per unit each wave DMAs its share of the CTA's [32][KR/32] scale
 //   block (4 bytes per lane); a barrier per unit publishes it.
+// * Panel weights (P): a unit's 32 columns are one panel, so a wave's unit is
+//   KW/64 consecutive 1 KB blocks already in MFMA lane order and the unit's
+//   scales are KR consecutive bytes: every DMA reads 1 KB of contiguous HBM
+//   and lands linearly in LDS, and the reads need no rotation.  The K order
+//   per lane is the [N,K/2] one, so both give identical results.
 // * Split-K without a serial tail.  CTA b = (jg, r) processes the S units
 //   (group S*jg + (u + r) % S, split r), u = 0 .. S-1, so every column group
 //   has exactly one unit at the last position u = S-1 (its "late" unit) and
@@ -111,8 +117,9 @@ __device__ __forceinline__ f32x4 packet_values(u32x4 a, u32x4 b) {
   return f32x4{fa.x, fa.z, fb.x, fb.z};
 }
 
-template <int MT, int WAVES, int GCB, int NSLOT, int SMAX, int KW>
-__global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_nk_kernel(StreamArgs p) {
+template <int LAYOUT, int MT, int WAVES, int GCB, int NSLOT, int SMAX, int KW>
+__global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs p) {
+  static_assert(LAYOUT == kLayoutNK || LAYOUT == kLayoutP, "weight layout");
   using Cfg = StreamCfg<MT, WAVES, GCB, NSLOT, KW>;
   constexpr int STEPS = Cfg::STEPS, CH = Cfg::CH, CPD = Cfg::CPD, NI = Cfg::NI;
   constexpr int GC = Cfg::GC, TILE = Cfg::TILE, NV = Cfg::NV, SLOT = Cfg::SLOT;
@@ -150,6 +157,22 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_nk_kernel(StreamAr
       const int sl = u % NSLOT;
       const int g = group_of(u);
       const bool live = g < p.groups;
+      if constexpr (LAYOUT == kLayoutP) {
+        // scales: the unit's KR/64 blocks of 64 bytes, consecutive
+        const desc_t ds = make_desc(p.S + (size_t)g * (K / kPK) * 64 + (size_t)r * Cfg::KR);
+#pragma unroll
+        for (int k = 0; k < Cfg::SC_LOADS; ++k) {
+          const int base = 256 * (Cfg::SC_LOADS * wave + k), byte = base + 4 * lane;
+          const bool ok = live && r * Cfg::KR + 64 * (byte >> 6) < K;
+          dma4(ds, scr + sl * Cfg::SC_UNIT + base, ok ? (uint32_t)byte : kOobOffset);
+        }
+        // weights: this wave's KW/64 consecutive 1 KB blocks of panel g
+        const desc_t d = make_desc(p.B + ((size_t)g * (K / kPK) + (kw0 >> 6)) * 1024);
+#pragma unroll
+        for (int i = 0; i < Cfg::W_LOADS; ++i)
+          dma16(d, wring + sl * SLOT + i * 1024, live && kok ? (uint32_t)(i * 1024 + 16 * lane) : kOobOffset);
+        return;
+      }
       // scales: the unit's [GC][KR/32] block, wave w moving bytes
       // [w*SC_UNIT/WAVES, ...) in 64-lane x 4-byte DMAs (4 groups per lane)
       {
@@ -248,6 +271,25 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_nk_kernel(StreamAr
       const uint8_t* ss = scr + sl * Cfg::SC_UNIT;
 #pragma unroll
       for (int cb = 0; cb < GCB; ++cb) {
+        if constexpr (LAYOUT == kLayoutP) {
+          // chunk j = 4t + q (K 32j of the wave's range): block j/2, lane slot
+          // 32 (j % 2) + column; its scale at the same position of the block's
+          // 64 scale bytes
+#pragma unroll
+          for (int t = 0; t < STEPS; ++t) {
+            const int blk = 2 * t + (q >> 1), slot = 32 * (q & 1) + 16 * cb + c;
+            const u32x4 wv = *reinterpret_cast<const u32x4*>(ws + blk * 1024 + slot * 16);
+            const float sc = e8m0_to_f32(ss[((wave * KW) / kPK + blk) * 64 + slot]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const bf16x8 b = operand_from_word(wv[s], sc);
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt)
+                acc[mt][cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a[mt][t][s]), b, acc[mt][cb]);
+            }
+          }
+          continue;
+        }
         // this wave's KW/32 scale bytes of the column: byte j scales chunk j
         uint32_t scw[STEPS];
         if constexpr (STEPS == 2) {
@@ -489,11 +531,18 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_nk_kernel(StreamAr
 }
 
 template <int MT, int WAVES, int GCB, int NSLOT, int SMAX, int KW>
-hipError_t launch_one(const StreamArgs& a, hipStream_t stream) {
+hipError_t launch_one(int layout, const StreamArgs& a, hipStream_t stream) {
   using Cfg = StreamCfg<MT, WAVES, GCB, NSLOT, KW>;
   if (a.splits < 1 || a.splits > SMAX) return hipErrorInvalidValue;
   const int grid = a.ctas;
-  hipLaunchKernelGGL((stream_nk_kernel<MT, WAVES, GCB, NSLOT, SMAX, KW>), dim3(grid), dim3(Cfg::NT), 0, stream, a);
+  if (layout == kLayoutNK)
+    hipLaunchKernelGGL((stream_kernel<kLayoutNK, MT, WAVES, GCB, NSLOT, SMAX, KW>), dim3(grid), dim3(Cfg::NT), 0,
+                       stream, a);
+  else if (layout == kLayoutP)
+    hipLaunchKernelGGL((stream_kernel<kLayoutP, MT, WAVES, GCB, NSLOT, SMAX, KW>), dim3(grid), dim3(Cfg::NT), 0,
+                       stream, a);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
@@ -516,10 +565,10 @@ bool stream_shape_available(const StreamShape& s) {
   return false;
 }
 
-hipError_t launch_stream(const StreamShape& s, const StreamArgs& args, hipStream_t stream) {
+hipError_t launch_stream(int layout, const StreamShape& s, const StreamArgs& args, hipStream_t stream) {
 #define X(MT_, W_, GCB_, NS_, SM_, KW_)                                                               \
   if (s.mt == MT_ && s.waves == W_ && s.gcb == GCB_ && s.nslot == NS_ && s.smax == SM_ && s.kw == KW_) \
-    return launch_one<MT_, W_, GCB_, NS_, SM_, KW_>(args, stream);
+    return launch_one<MT_, W_, GCB_, NS_, SM_, KW_>(layout, args, stream);
   MXFP4_STREAM_SHAPES(X)
 #undef X
   return hipErrorInvalidValue;

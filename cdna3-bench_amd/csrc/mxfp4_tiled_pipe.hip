@@ -23,6 +23,14 @@
 //     WNC*c + j and the epilogue writes WNC adjacent columns per lane.
 //   [N,K/2] weights: a lane reads 16 bytes = 32 K of column block cb; word s
 //     against the A chunk K 32h + 8s .. +7.
+//   G (128-column prepack): the [K/2,N] lane map with words instead of bytes:
+//     a stage of a 128-column block is 8 chunk rows x 512 bytes, contiguous
+//     in HBM and in LDS; a lane reads the WNC adjacent words of its columns
+//     in chunk 2ks + h (one 16- or 8-byte read) and MFMA j converts word j.
+//     The MFMA operands equal the [K/2,N] kernel's exactly.
+//   P (panels): the [N,K/2] lane map; a stage of a 32-column panel is one
+//     1 KB block already in lane order, so the DMA and the LDS read are both
+//     linear (no swizzle) and the MFMA operands equal the [N,K/2] kernel's.
 //
 // Reference counterpart: the K loop of strategy_j/strategy_m
 // (csrc/strategy_j_synthesis.cu:120-170, csrc/strategy_m_asm.cu:131-185),
@@ -49,7 +57,8 @@ struct PipeCfg {
   // E8M0 scales of a stage also go through LDS: [K/2,N]: the stage's two K
   // group rows of BN bytes; [N,K/2]: per column the aligned dword holding its
   // two groups (needs K % 128 == 0).  One 64-lane x 4-byte DMA per wave.
-  static constexpr int SC_BYTES = LAYOUT == kLayoutKN ? 2 * BN : 4 * BN;
+  //   G, P: two groups per column as well, 256 bytes per 128 columns.
+  static constexpr int SC_BYTES = LAYOUT == kLayoutNK ? 4 * BN : 2 * BN;
   static constexpr int SC_INSTR = SC_BYTES / 256;
   static constexpr int STAGE = A_BYTES + B_BYTES + SC_BYTES;
   static constexpr int A_INSTR = A_BYTES / 1024;
@@ -61,6 +70,7 @@ struct PipeCfg {
   // LDS DMAs one wave issues per stage (A, B, one scale DMA).
   static constexpr int VM_PER_ITER = A_PER_WAVE + B_PER_WAVE + 1;
   static constexpr int KN_CPR = BN / 16;  // 16-byte chunks per K-pair row
+  static_assert(LAYOUT != kLayoutG || (BN % kGCols == 0 && WCOLS <= kGCols), "G: whole 128-column blocks");
 };
 
 template <int LAYOUT, int RB, int WNC>
@@ -76,6 +86,22 @@ template <int RB, int WNC>
 struct SubOps<kLayoutNK, RB, WNC> {
   bf16x8 a[RB];
 };
+
+template <int RB, int WNC>
+struct SubOps<kLayoutG, RB, WNC> {
+  bf16x8 a[RB];
+  uint32_t raw[WNC];  // word of column WNC*c + j in chunk 2ks + h
+};
+
+template <int RB, int WNC>
+struct SubOps<kLayoutP, RB, WNC> {
+  bf16x8 a[RB];
+};
+
+// Layouts whose lanes follow the [K/2,N] map (WNC adjacent columns per lane)
+// or the [N,K/2] map (one column per column block, 32 K per lane).
+template <int L>
+constexpr bool kColumnWords = L == kLayoutKN || L == kLayoutG;
 
 template <int LAYOUT, int WM, int WN, int RB, int WNC, int NS>
 __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p) {
@@ -139,7 +165,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
         const bool ok = live && ((k0 >> 1) + row < Kh) && (n0 + lc * 16 < N);
         dma16(rb, sB + i * 1024, ok ? (uint32_t)(row * N + lc * 16) : kOobOffset);
       }
-    } else {
+    } else if constexpr (LAYOUT == kLayoutNK) {
       const desc_t rb = make_desc(p.B + (size_t)n0 * Kh + (k0 >> 1));
 #pragma unroll
       for (int ii = 0; ii < Cfg::B_PER_WAVE; ++ii) {
@@ -149,6 +175,28 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
         const int lc = (q & 1) ^ ((row >> 2) & 1);  // rows with bit 2 set swap their chunks
         const bool ok = live && (n0 + row < N) && ((k0 >> 1) + lc * 16 < Kh);
         dma16(rb, sB + i * 1024, ok ? (uint32_t)(row * Kh + lc * 16) : kOobOffset);
+      }
+    } else if constexpr (LAYOUT == kLayoutG) {
+      // block nbl's stage: chunks k0/8 .. k0/8 + 7 x 128 columns x 4 bytes
+      const uint32_t blk = (uint32_t)Kh * kGCols;  // bytes per 128-column block
+      const desc_t rb = make_desc(p.B + (size_t)(n0 / kGCols) * blk + (size_t)step * 4096);
+#pragma unroll
+      for (int ii = 0; ii < Cfg::B_PER_WAVE; ++ii) {
+        const int i = wave * Cfg::B_PER_WAVE + ii;
+        const int byte = i * 1024 + 16 * lane;
+        const int nbl = byte >> 12, w = byte & 4095;
+        const bool ok = live && (n0 + nbl * kGCols < N) && (k0 + 8 * (w >> 9) < K);
+        dma16(rb, sB + i * 1024, ok ? (uint32_t)(nbl * blk + w) : kOobOffset);
+      }
+    } else {
+      // panel i's stage: one 1 KB block
+      const uint32_t pan = (uint32_t)Kh * kPCols;  // bytes per panel
+      const desc_t rb = make_desc(p.B + (size_t)(n0 / kPCols) * pan + (size_t)step * 1024);
+#pragma unroll
+      for (int ii = 0; ii < Cfg::B_PER_WAVE; ++ii) {
+        const int i = wave * Cfg::B_PER_WAVE + ii;
+        const bool ok = live && (n0 + i * kPCols < N) && (k0 < K);
+        dma16(rb, sB + i * 1024, ok ? (uint32_t)(i * pan + 16 * lane) : kOobOffset);
       }
     }
     // scales: wave w < SC_INSTR loads bytes 256w .. 256w+255 of the stage's scale block
@@ -161,11 +209,25 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
       const int row = byte / BN, col = byte % BN;
       const bool ok = live && sc_wave && (g0 + row < G) && (n0 + col < N);
       dma4(rs, sc_wave ? sC + 256 * wave : smem + NS * Cfg::STAGE, ok ? (uint32_t)(row * N + col) : kOobOffset);
-    } else {
+    } else if constexpr (LAYOUT == kLayoutNK) {
       const desc_t rs = make_desc(p.S + (size_t)n0 * G + (g0 & ~3));
       const int n = 64 * wave + lane;
       const bool ok = live && sc_wave && (n0 + n < N) && (g0 < G);
       dma4(rs, sc_wave ? sC + 256 * wave : smem + NS * Cfg::STAGE, ok ? (uint32_t)(n * G) : kOobOffset);
+    } else if constexpr (LAYOUT == kLayoutG) {
+      // wave w: block w's groups g0, g0 + 1 (2 x 128 bytes) -> sC[w][2][128]
+      const desc_t rs = make_desc(p.S + ((size_t)(n0 / kGCols) * G + g0) * kGCols);
+      const int g = lane >> 5, ni = (4 * lane) & 127;
+      const bool ok = live && sc_wave && (n0 + wave * kGCols < N) && (g0 + g < G);
+      dma4(rs, sc_wave ? sC + 256 * wave : smem + NS * Cfg::STAGE,
+           ok ? (uint32_t)(wave * G * kGCols + g * kGCols + ni) : kOobOffset);
+    } else {
+      // wave w: the stage's 64-byte blocks of panels 4w .. 4w + 3 -> sC[panel][64]
+      const desc_t rs = make_desc(p.S + (size_t)(n0 / kPCols) * (K / kPK) * 64 + (size_t)step * 64);
+      const int i = 4 * wave + (lane >> 4);
+      const bool ok = live && sc_wave && (n0 + i * kPCols < N) && (k0 < K);
+      dma4(rs, sc_wave ? sC + 256 * wave : smem + NS * Cfg::STAGE,
+           ok ? (uint32_t)(i * (K / kPK) * 64 + 4 * (lane & 15)) : kOobOffset);
     }
   };
 
@@ -176,19 +238,26 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
     const int row = wm * RB * 32 + c;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int lc = LAYOUT == kLayoutKN ? ks * 2 + h : h * 4 + ks;
+      const int lc = kColumnWords<LAYOUT> ? ks * 2 + h : h * 4 + ks;
       a_off[ks] = (uint32_t)(row * 128 + ((lc ^ a_swz(row)) * 16));
     }
   }
   // B: [K/2,N] row ks*8 + 4h + i (its swizzle depends on h only);
   //    [N,K/2] row wn*WCOLS + 32*cb + c (its swizzle depends on c only).
+  //    G: block col/128, chunk 2ks + h, word col%128 (col = wn*WCOLS + WNC*c);
+  //    P: panel wn*WNC + cb, lane slot 32h + c.
   uint32_t b_off;
   if constexpr (LAYOUT == kLayoutKN) {
     constexpr int CPR = Cfg::KN_CPR;
     const int byte = wn * WCOLS + WNC * c;
     b_off = (uint32_t)(Cfg::A_BYTES + h * 4 * BN + (((byte >> 4) ^ (h * (CPR / 2))) * 16) + (byte & 15));
-  } else {
+  } else if constexpr (LAYOUT == kLayoutNK) {
     b_off = (uint32_t)(Cfg::A_BYTES + (wn * WCOLS + c) * 32 + ((h ^ ((c >> 2) & 1)) * 16));
+  } else if constexpr (LAYOUT == kLayoutG) {
+    const int col = wn * WCOLS + WNC * c;
+    b_off = (uint32_t)(Cfg::A_BYTES + (col >> 7) * 4096 + h * 512 + (col & 127) * 4);
+  } else {
+    b_off = (uint32_t)(Cfg::A_BYTES + wn * WNC * 1024 + (32 * h + c) * 16);
   }
 
   // ---- LDS -> registers ------------------------------------------------------
@@ -211,13 +280,25 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
         o.raw[0] = r0 | (r1 << 16);
         o.raw[1] = r2 | (r3 << 16);
       }
+    } else if constexpr (LAYOUT == kLayoutG) {
+      const uint8_t* pb = base + b_off + ks * 1024;
+      if constexpr (WNC == 4) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(pb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o.raw[j] = v[j];
+      } else {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(pb);
+        o.raw[0] = v.x;
+        o.raw[1] = v.y;
+      }
     }
   };
-  // [N,K/2]: the column blocks' 16 bytes for the whole stage.
+  // [N,K/2], P: the column blocks' 16 bytes for the whole stage (column
+  // blocks are 1 KB apart in both LDS images).
   auto read_braw = [&](int buf, u32x4 (&raw)[WNC]) {
     const uint8_t* base = smem + buf * Cfg::STAGE + b_off;
 #pragma unroll
-    for (int cb = 0; cb < WNC; ++cb) raw[cb] = *reinterpret_cast<const u32x4*>(base + cb * 32 * 32);
+    for (int cb = 0; cb < WNC; ++cb) raw[cb] = *reinterpret_cast<const u32x4*>(base + cb * 1024);
   };
 
   f32x16 acc[RB][WNC];
@@ -230,7 +311,14 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
 
   // cvt + MFMA for one sub-step; sc = the column scales of its K group.
   auto mma_kn = [&](const Ops& o, const float (&sc)[WNC]) {
-    if constexpr (LAYOUT != kLayoutKN) {
+    if constexpr (LAYOUT == kLayoutG) {
+#pragma unroll
+      for (int j = 0; j < WNC; ++j) {
+        const bf16x8 b = operand_from_word(o.raw[j], sc[j]);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[rb][j] = mfma_32x32x16(o.a[rb], b, acc[rb][j]);
+      }
+    } else if constexpr (LAYOUT != kLayoutKN) {
       (void)o;
       (void)sc;
     } else if constexpr (WNC == 4) {
@@ -284,24 +372,29 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
     Ops cur, nxt;
     u32x4 braw_cur[WNC], braw_nxt[WNC];
     read_ops(0, 0, cur);
-    if constexpr (LAYOUT == kLayoutNK) read_braw(0, braw_cur);
+    if constexpr (!kColumnWords<LAYOUT>) read_braw(0, braw_cur);
 
     for (int t = 0; t < T; ++t) {
       const int buf = t % NS;
       load_stage((t + NS - 1) % NS, s_begin + t + NS - 1, t + NS - 1 < T);
       // this stage's scales (published with its data)
       const uint8_t* sC = smem + buf * Cfg::STAGE + Cfg::A_BYTES + Cfg::B_BYTES;
-      float sf[WNC];       // [N,K/2]: per column block
-      float skn[2][WNC];   // [K/2,N]: per K group, per byte column
+      float sf[WNC];       // [N,K/2], P: per column block
+      float skn[2][WNC];   // [K/2,N], G: per K group, per column of the lane
       if constexpr (LAYOUT == kLayoutNK) {
         const int shift = 8 * (((2 * (s_begin + t)) & 2) + h);
 #pragma unroll
         for (int cb = 0; cb < WNC; ++cb)
           sf[cb] = e8m0_to_f32(*reinterpret_cast<const uint32_t*>(sC + 4 * (wn * WCOLS + 32 * cb + c)) >> shift);
+      } else if constexpr (LAYOUT == kLayoutP) {
+#pragma unroll
+        for (int cb = 0; cb < WNC; ++cb) sf[cb] = e8m0_to_f32(sC[(wn * WNC + cb) * 64 + 32 * h + c]);
       } else {
+        const int col = wn * WCOLS + WNC * c;
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-          const uint8_t* row = sC + g * BN + wn * WCOLS + WNC * c;
+          const uint8_t* row = LAYOUT == kLayoutKN ? sC + g * BN + col
+                                                   : sC + (col >> 7) * 256 + g * kGCols + (col & 127);
           const uint32_t w = WNC == 4 ? *reinterpret_cast<const uint32_t*>(row)
                                       : (uint32_t)*reinterpret_cast<const uint16_t*>(row);
 #pragma unroll
@@ -311,7 +404,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
 #pragma unroll
       for (int ks = 0; ks < 3; ++ks) {
         read_ops(buf, ks + 1, nxt);
-        if constexpr (LAYOUT == kLayoutKN)
+        if constexpr (kColumnWords<LAYOUT>)
           mma_kn(cur, skn[ks >> 1]);
         else
           mma_nk(cur, braw_cur, sf, ks);
@@ -323,13 +416,13 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
       __syncthreads();
       // Past the last step this reads a stage of OOB zeros; the values are unused.
       read_ops((t + 1) % NS, 0, nxt);
-      if constexpr (LAYOUT == kLayoutNK) read_braw((t + 1) % NS, braw_nxt);
-      if constexpr (LAYOUT == kLayoutKN)
+      if constexpr (!kColumnWords<LAYOUT>) read_braw((t + 1) % NS, braw_nxt);
+      if constexpr (kColumnWords<LAYOUT>)
         mma_kn(cur, skn[1]);
       else
         mma_nk(cur, braw_cur, sf, 3);
       cur = nxt;
-      if constexpr (LAYOUT == kLayoutNK) {
+      if constexpr (!kColumnWords<LAYOUT>) {
 #pragma unroll
         for (int cb = 0; cb < WNC; ++cb) braw_cur[cb] = braw_nxt[cb];
       }
@@ -377,7 +470,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
     for (int i = 0; i < 16; ++i) {
       const int row = m0 + wm * RB * 32 + rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
       if (row >= M) continue;
-      if constexpr (LAYOUT == kLayoutKN) {
+      if constexpr (kColumnWords<LAYOUT>) {
         const int col = n0 + wn * WCOLS + WNC * c;
         if (col >= N) continue;
         if constexpr (WNC == 4) {
@@ -455,9 +548,13 @@ bool tiled_pipe_shape_available(int layout, const TiledShape& s) {
 
 hipError_t launch_tiled_pipe(int layout, const TiledShape& shape, const TiledArgs& args,
                              hipStream_t stream) {
-  if (layout == kLayoutKN) return dispatch_shape<kLayoutKN>(shape, args, stream);
-  if (layout == kLayoutNK) return dispatch_shape<kLayoutNK>(shape, args, stream);
-  return hipErrorInvalidValue;
+  switch (layout) {
+    case kLayoutKN: return dispatch_shape<kLayoutKN>(shape, args, stream);
+    case kLayoutNK: return dispatch_shape<kLayoutNK>(shape, args, stream);
+    case kLayoutG: return dispatch_shape<kLayoutG>(shape, args, stream);
+    case kLayoutP: return dispatch_shape<kLayoutP>(shape, args, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace mxfp4

@@ -8,11 +8,13 @@ module raises if the extension is missing, as the reference does
 Reference functions and their counterparts:
   gemm_a .. gemm_m  (kernels.py:35-94)  same names/arguments/accepted shapes;
                                         all run the library's chosen plan
-  gemm_g            (kernels.py:59-60)  prepacked (strategy G) layout
+  gemm_g            (kernels.py:59-60)  prepacked (strategy G) layout, read directly
   gemm_auto         (kernels.py:63-74)  every shape with K % 32 == 0
   device_info, shape_supported_{c,d,e,f,g} (kernels.py:11-32)
-Additions: ``gemm`` (either weight layout, bf16/fp32 out, explicit plan),
-``dequantize`` (device dequant tile), ``select_plan``.
+Additions: ``gemm`` (any weight layout, bf16/fp32 out, explicit plan),
+``dequantize`` (device dequant tile), ``prepack`` / ``convert_layout``
+(device counterpart of ref.py:85-101 ``prepack_b_mxfp4``, between any two
+layouts), ``select_plan``.
 """
 
 import torch  # noqa: F401  (loads the HIP runtime symbols _C links against)
@@ -26,6 +28,8 @@ except ImportError as e:  # pragma: no cover - exercised only without a build
 
 LAYOUT_KN = "kn"  # B [K/2, N], S [K/32, N]  (reference API layout)
 LAYOUT_NK = "nk"  # B [N, K/2], S [N, K/32]  (K-contiguous weights)
+LAYOUT_G = "g"    # B [N/128, K/8, 128, 4], S [N/128, K/32, 128]  (strategy G prepack, N % 128 == 0)
+LAYOUT_P = "p"    # B [N/32, K/64, 2, 32, 16], S [N/32, K/64, 2, 32]  (panels, N % 32 == 0, K % 64 == 0)
 
 KERNEL_AUTO, KERNEL_GEMV, KERNEL_TILED, KERNEL_GENERIC, KERNEL_STREAM = 0, 1, 2, 3, 4
 
@@ -108,7 +112,8 @@ def gemm_auto(A, B_packed, B_scales, C=None):
 
 
 def gemm(A, B, S, C=None, layout=LAYOUT_KN, out_dtype=None, plan=None):
-    """C = A @ dequant(B, S) in either weight layout.
+    """C = A @ dequant(B, S) in any weight layout (g / p: any shape of the
+    layout's size, N = B.numel() / (K/2)).
 
     out_dtype: torch.float32 (default) or torch.bfloat16 when C is None.
     plan: optional (kernel, variant, split_k) overriding the cost model.
@@ -116,9 +121,27 @@ def gemm(A, B, S, C=None, layout=LAYOUT_KN, out_dtype=None, plan=None):
     return _ext.gemm(A, B, S, C, layout, out_dtype, None if plan is None else list(plan))
 
 
-def dequantize(B, S, layout=LAYOUT_KN, out_dtype=torch.bfloat16):
-    """Dequantized weights [K, N] on the device (bf16 or fp32)."""
-    return _ext.dequant(B, S, layout, out_dtype)
+def dequantize(B, S, layout=LAYOUT_KN, out_dtype=torch.bfloat16, K=None):
+    """Dequantized weights [K, N] on the device (bf16 or fp32).  K is needed
+    only for flat g / p weights."""
+    return _ext.dequant(B, S, layout, out_dtype, K)
+
+
+def convert_layout(B, S, src, dst, K=None):
+    """(codes, scales) of the same weights in layout ``dst``, rewritten on the
+    device.  K is needed only for flat g / p sources."""
+    return _ext.convert_layout(B, S, src, dst, K)
+
+
+def prepack(B_packed, B_scales, layout=LAYOUT_P):
+    """Device prepack of reference-layout weights ([K/2, N], [K/32, N]).
+
+    layout "g" gives the strategy-G arrays of ref.py:85-101 (flattened, as
+    ``prepack_b_mxfp4`` returns them, ready for ``gemm_g``); "p" (default)
+    the panel layout the MI355X kernels prefer.
+    """
+    Bp, Sp = _ext.convert_layout(B_packed, B_scales, LAYOUT_KN, layout, None)
+    return (Bp.reshape(-1), Sp.reshape(-1)) if layout == LAYOUT_G else (Bp, Sp)
 
 
 def select_plan(M, N, K, layout=LAYOUT_KN):

@@ -16,7 +16,18 @@
  *       MXFP4_LAYOUT_KN: B [K/2, N], S [K/32, N]   (reference API layout,
  *                        csrc/mxfp4_ext.cpp:21-24)
  *       MXFP4_LAYOUT_NK: B [N, K/2], S [N, K/32]   (K-contiguous weights)
- *   - K % 32 == 0 (csrc/mxfp4_ext.cpp:28).  Any M >= 0, N >= 0.
+ *       MXFP4_LAYOUT_G:  B [N/128][K/8][128][4], S [N/128][K/32][128]
+ *                        (strategy G prepack, python/mxfp4_cdna3/ref.py:85-101;
+ *                        needs N % 128 == 0)
+ *       MXFP4_LAYOUT_P:  B [N/32][K/64][2][32][16], S [N/32][K/64][2][32]
+ *                        (panels: each 32-column x 64-K block of codes is 1 KB
+ *                        in wave-lane order -- 16 bytes = 32 K of one column
+ *                        per lane -- with its 64 scale bytes in the same lane
+ *                        order; needs N % 32 == 0 and K % 64 == 0)
+ *     In every layout packed byte kp of column n holds K = 2kp and 2kp + 1 of
+ *     that column, and scale byte g scales K = 32g .. 32g + 31.
+ *   - K % 32 == 0 (csrc/mxfp4_ext.cpp:28).  Any M >= 0, N >= 0 within the
+ *     layout's rule above.
  *   - Launches are asynchronous on `stream`; nothing synchronizes.
  *   - Return value is a hipError_t: hipSuccess, hipErrorInvalidValue for bad
  *     arguments (same convention as the reference launchers, e.g.
@@ -35,14 +46,14 @@
 extern "C" {
 #endif
 
-enum { MXFP4_LAYOUT_KN = 0, MXFP4_LAYOUT_NK = 1 };
+enum { MXFP4_LAYOUT_KN = 0, MXFP4_LAYOUT_NK = 1, MXFP4_LAYOUT_G = 2, MXFP4_LAYOUT_P = 3 };
 enum { MXFP4_OUT_F32 = 0, MXFP4_OUT_BF16 = 1 };
 enum {
   MXFP4_KERNEL_AUTO = 0,    /* cost-model choice */
   MXFP4_KERNEL_GEMV = 1,    /* memory-bound family, M <= 32 */
   MXFP4_KERNEL_TILED = 2,   /* MFMA-bound tiled family */
   MXFP4_KERNEL_GENERIC = 3, /* one thread per output, any N */
-  MXFP4_KERNEL_STREAM = 4   /* split-K weight streaming, M <= 32, [N,K/2], K % 256 == 0 */
+  MXFP4_KERNEL_STREAM = 4   /* split-K weight streaming, M <= 32, NK or P layout, K % 256 == 0 */
 };
 
 /* A launch plan: which kernel family, which tile variant, how many K splits. */
@@ -107,6 +118,19 @@ hipError_t mxfp4_gemm_with_plan(const void* A, const uint8_t* B, const uint8_t* 
  */
 hipError_t mxfp4_dequant(const uint8_t* B, const uint8_t* S, void* out, int out_dtype, int64_t K,
                          int64_t N, int b_layout, hipStream_t stream);
+
+/*
+ * Rewrites weights (codes B, scales S) of a K x N matrix from one layout to
+ * another on the device: B_out/S_out receive the same bytes at the positions
+ * of dst_layout.  Device counterpart of prepack_b_mxfp4
+ * (python/mxfp4_cdna3/ref.py:85-101, which the reference runs on the host
+ * before upload); any pair of MXFP4_LAYOUT_* works, including the inverse
+ * direction.  Both layouts' shape rules apply.  Sources and destinations
+ * must not overlap; B_out 16-byte aligned.
+ */
+hipError_t mxfp4_convert_layout(const uint8_t* B, const uint8_t* S, int src_layout, uint8_t* B_out,
+                                uint8_t* S_out, int dst_layout, int64_t K, int64_t N,
+                                hipStream_t stream);
 
 /*
  * The reference's shape predicates (csrc/common.h:80-99), strategy 'c'..'g'

@@ -32,8 +32,13 @@ How each function is pinned (tests/test_oracle.py):
 * GEMM: brute-force Python loops on tiny shapes, closed-form special cases
   (all-zero codes, all-ones codes = row sums, one nonzero K group), and the
   C restatement's float64 GEMM.
-* ``prepack_b_mxfp4``: bijection (every byte lands exactly once) and the
-  inverse permutation.
+* ``prepack_b_mxfp4``: bijection (every byte lands exactly once), the
+  inverse permutation and element positions read off ref.py:86-94.
+* ``panel_pack`` (the MI355X panel layout, no reference counterpart):
+  bijection, inverse, element positions from its definition computed by
+  plain-Python index loops, and the C++ index functions of the device code
+  (cdna3-bench_amd/csrc/mxfp4_layout.h, compiled with g++) agree with it for
+  every byte of small shapes, for all four layouts.
 * ``quantize_mxfp4``: the reference's own KATs (tests/test_smoke.py:6-28).
   Its argmin tie-breaking (first minimum, i.e. toward the smaller magnitude)
   follows numpy's documented argmin semantics; beyond those KATs it is
@@ -56,6 +61,8 @@ E2M1_MAGNITUDES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], dtype=np.fl
 # Layout tags shared with the C-ABI (include/mxfp4_mi355x.h).
 LAYOUT_KN = 0  # reference API: B_packed [K/2, N], B_scales [K/32, N]
 LAYOUT_NK = 1  # W [N, K/2], S [N, K/32]
+LAYOUT_G = 2   # strategy G prepack (ref.py:85-101, n_tile 128)
+LAYOUT_P = 3   # panels: [N/32][K/64][2][32][16] codes, [N/32][K/64][2][32] scales
 
 
 # ---------------------------------------------------------------------------
@@ -224,6 +231,56 @@ def unprepack_b_mxfp4(B_prep, Bs_prep, K, N, n_tile=128):
     bp = np.asarray(B_prep).reshape(nb, K // 8, n_tile, 4).transpose(1, 3, 0, 2).reshape(K // 2, N)
     bs = np.asarray(Bs_prep).reshape(nb, K // 32, n_tile).transpose(1, 0, 2).reshape(K // 32, N)
     return np.ascontiguousarray(bp), np.ascontiguousarray(bs)
+
+
+def panel_pack(B_packed, B_scales):
+    """[K/2, N], [K/32, N] -> the panel layout (flat codes, flat scales).
+
+    P[p, t, h, c, j] = B_packed[32t + 16h + j, 32p + c]   (K = 64t + 32h + 2j, 2j+1)
+    Ps[p, t, h, c]   = B_scales[2t + h, 32p + c]
+    i.e. each 32-column x 64-K block is 1 KB in which lane 32h + c holds the
+    16 bytes (32 K) of column c, and its 64 scale bytes in the same lane order.
+    """
+    Kh, N = B_packed.shape
+    K = Kh * 2
+    if N % 32 or K % 64:
+        raise ValueError("panel layout needs N % 32 == 0 and K % 64 == 0")
+    bp = np.ascontiguousarray(B_packed).reshape(K // 64, 2, 16, N // 32, 32).transpose(3, 0, 1, 4, 2)
+    bs = np.ascontiguousarray(B_scales).reshape(K // 64, 2, N // 32, 32).transpose(2, 0, 1, 3)
+    return np.ascontiguousarray(bp).reshape(-1), np.ascontiguousarray(bs).reshape(-1)
+
+
+def panel_unpack(P, Ps, K, N):
+    """Inverse of ``panel_pack``."""
+    bp = np.asarray(P).reshape(N // 32, K // 64, 2, 32, 16).transpose(1, 2, 4, 0, 3).reshape(K // 2, N)
+    bs = np.asarray(Ps).reshape(N // 32, K // 64, 2, 32).transpose(1, 2, 0, 3).reshape(K // 32, N)
+    return np.ascontiguousarray(bp), np.ascontiguousarray(bs)
+
+
+def to_layout(B_kn, S_kn, layout):
+    """Reference-layout weights in ``layout`` (G and P flat, as the packers return them)."""
+    if layout == LAYOUT_KN:
+        return np.ascontiguousarray(B_kn), np.ascontiguousarray(S_kn)
+    if layout == LAYOUT_NK:
+        return kn_to_nk(B_kn, S_kn)
+    if layout == LAYOUT_G:
+        return prepack_b_mxfp4(B_kn, S_kn)
+    if layout == LAYOUT_P:
+        return panel_pack(B_kn, S_kn)
+    raise ValueError(layout)
+
+
+def from_layout(B, S, layout, K, N):
+    """Weights in ``layout`` -> reference layout [K/2, N], [K/32, N]."""
+    if layout == LAYOUT_KN:
+        return np.asarray(B).reshape(K // 2, N), np.asarray(S).reshape(K // 32, N)
+    if layout == LAYOUT_NK:
+        return nk_to_kn(np.asarray(B).reshape(N, K // 2), np.asarray(S).reshape(N, K // 32))
+    if layout == LAYOUT_G:
+        return unprepack_b_mxfp4(B, S, K, N)
+    if layout == LAYOUT_P:
+        return panel_unpack(B, S, K, N)
+    raise ValueError(layout)
 
 
 # ---------------------------------------------------------------------------

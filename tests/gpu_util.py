@@ -25,10 +25,15 @@ def to_dev_u8(x):
     return torch.from_numpy(np.ascontiguousarray(x)).cuda()
 
 
+LAYOUT_TAGS = {"kn": mo.LAYOUT_KN, "nk": mo.LAYOUT_NK, "g": mo.LAYOUT_G, "p": mo.LAYOUT_P}
+
+
 def weights_for_layout(W_nk, S_nk, layout):
+    """[N, K/2] weights in ``layout`` (g and p flat, as the oracle packers give them)."""
     if layout == "nk":
         return W_nk, S_nk
-    return mo.nk_to_kn(W_nk, S_nk)
+    B, S = mo.nk_to_kn(W_nk, S_nk)
+    return mo.to_layout(B, S, LAYOUT_TAGS[layout])
 
 
 def run_gemm(kk, A_bits, W_nk, S_nk, layout="kn", out_dtype=None, plan=None):
