@@ -485,6 +485,18 @@ hipError_t mxfp4_convert_layout(const uint8_t* B, const uint8_t* S, int src_layo
   return launch_convert(src_layout, dst_layout, B, S, B_out, S_out, (size_t)K, (size_t)N, stream);
 }
 
+hipError_t mxfp4_quantize(const void* X, int x_dtype, int x_layout, int64_t K, int64_t N, uint8_t* B,
+                          uint8_t* S, int b_layout, hipStream_t stream) {
+  if (K < 0 || N < 0 || K % 32 != 0) return hipErrorInvalidValue;
+  if (x_dtype != MXFP4_IN_F32 && x_dtype != MXFP4_IN_BF16) return hipErrorInvalidValue;
+  if (x_layout != kLayoutKN && x_layout != kLayoutNK) return hipErrorInvalidValue;
+  if (!layout_ok(b_layout, N, K)) return hipErrorInvalidValue;
+  if (K * N == 0) return hipSuccess;
+  if (!X || !B || !S || !aligned16(X) || !aligned16(B)) return hipErrorInvalidValue;
+  if ((uint64_t)(K / 32) * (uint64_t)N / 256 >= (1ull << 31)) return hipErrorInvalidValue;  // grid size
+  return launch_quantize(X, x_dtype == MXFP4_IN_BF16, x_layout, B, S, b_layout, (size_t)K, (size_t)N, stream);
+}
+
 int mxfp4_shape_supported(char strategy, int64_t M, int64_t N, int64_t K) {
   int bm, bn, bk = 64;
   switch (strategy) {

@@ -11,8 +11,9 @@
 // the others raise "Strategy X requires ..."), and all of them run the one
 // gfx950 path chosen by the library's cost model; gemm_g reads the G
 // prepack directly.  Additions: gemm_auto (every shape with K % 32 == 0),
-// gemm (any weight layout, explicit plan), dequant, convert_layout (device
-// prepack between layouts), select_plan.  C may be fp32 (the reference's
+// gemm (any weight layout, explicit plan), dequant, quantize (device
+// quantize_mxfp4), convert_layout (device prepack between layouts),
+// select_plan.  C may be fp32 (the reference's
 // only dtype) or bf16.
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
@@ -284,6 +285,34 @@ py::tuple convert_layout(const torch::Tensor& B, const torch::Tensor& S, const s
   return py::make_tuple(Bo, So);
 }
 
+// Device quantize_mxfp4 (python/mxfp4_cdna3/ref.py:14-47) of a 2-D fp32 / bf16
+// weight: axis 0 -> X is [K, N]; axis -1 (or 1) -> X is [N, K].  Output
+// layout default: "kn" for axis 0 and "nk" for axis -1, the shapes the
+// reference returns; any layout may be asked for.
+py::tuple quantize(const torch::Tensor& X, int64_t axis, c10::optional<std::string> layout) {
+  TORCH_CHECK(X.is_cuda(), "X must be on GPU");
+  TORCH_CHECK(X.dim() == 2, "X must be 2-D");
+  TORCH_CHECK(X.scalar_type() == at::kFloat || X.scalar_type() == at::kBFloat16, "X must be float32 or bfloat16");
+  TORCH_CHECK(X.is_contiguous(), "X must be contiguous");
+  TORCH_CHECK(axis == 0 || axis == 1 || axis == -1, "axis must be 0 or -1");
+  const bool kn_in = axis == 0;
+  const int64_t K = kn_in ? X.size(0) : X.size(1), N = kn_in ? X.size(1) : X.size(0);
+  TORCH_CHECK(K % 32 == 0, "axis ", axis, " length ", K, " not divisible by 32");
+  const int ld = layout.has_value() ? layout_code(*layout) : (kn_in ? MXFP4_LAYOUT_KN : MXFP4_LAYOUT_NK);
+  TORCH_CHECK(ld != MXFP4_LAYOUT_G || N % 128 == 0, "layout g needs N % 128 == 0");
+  TORCH_CHECK(ld != MXFP4_LAYOUT_P || (N % 32 == 0 && K % 64 == 0), "layout p needs N % 32 == 0 and K % 64 == 0");
+  auto opts = X.options().dtype(at::kByte);
+  torch::Tensor B = torch::empty(code_shape(ld, K, N), opts);
+  torch::Tensor S = torch::empty(scale_shape(ld, K, N), opts);
+  auto stream = c10::hip::getCurrentHIPStream(X.get_device()).stream();
+  hipError_t err = mxfp4_quantize(X.data_ptr(), X.scalar_type() == at::kBFloat16 ? MXFP4_IN_BF16 : MXFP4_IN_F32,
+                                  kn_in ? MXFP4_LAYOUT_KN : MXFP4_LAYOUT_NK, K, N,
+                                  static_cast<uint8_t*>(B.data_ptr()), static_cast<uint8_t*>(S.data_ptr()), ld,
+                                  stream);
+  TORCH_CHECK(err == hipSuccess, "mxfp4_quantize: ", hipGetErrorString(err));
+  return py::make_tuple(B, S);
+}
+
 torch::Tensor dequant(const torch::Tensor& B, const torch::Tensor& S, const std::string& layout,
                       at::ScalarType out_dtype, c10::optional<int64_t> K_opt) {
   const int lay = layout_code(layout);
@@ -363,6 +392,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("layout") = "kn", py::arg("out_dtype") = py::none(), py::arg("plan") = py::none());
   m.def("dequant", &dequant, py::arg("B"), py::arg("S"), py::arg("layout") = "kn",
         py::arg("out_dtype") = at::kBFloat16, py::arg("K") = py::none());
+  m.def("quantize", &quantize, py::arg("X"), py::arg("axis") = -1, py::arg("layout") = py::none());
   m.def("convert_layout", &convert_layout, py::arg("B"), py::arg("S"), py::arg("src"), py::arg("dst"),
         py::arg("K") = py::none());
   m.def("select_plan", &select_plan, py::arg("M"), py::arg("N"), py::arg("K"), py::arg("layout") = "kn");

@@ -120,6 +120,10 @@ hipError_t launch_dequant(int layout, const uint8_t* B, const uint8_t* S, void* 
 hipError_t launch_convert(int src_layout, int dst_layout, const uint8_t* B, const uint8_t* S,
                           uint8_t* B_out, uint8_t* S_out, size_t K, size_t N, hipStream_t stream);
 
+// fp32 / bf16 weights (X [K,N] or [N,K]) -> MXFP4 codes and scales in b_layout.
+hipError_t launch_quantize(const void* X, int x_bf16, int x_layout, uint8_t* B, uint8_t* S, int b_layout,
+                           size_t K, size_t N, hipStream_t stream);
+
 // C = 0 (K == 0).
 hipError_t launch_zero_fill(void* C, size_t bytes, hipStream_t stream);
 

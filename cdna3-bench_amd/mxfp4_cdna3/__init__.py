@@ -12,7 +12,7 @@ __version__ = "0.1.0"
 
 _KERNEL_NAMES = (
     "gemm_a", "gemm_b", "gemm_c", "gemm_d", "gemm_e", "gemm_f", "gemm_g", "gemm_h",
-    "gemm_i", "gemm_j", "gemm_k", "gemm_m", "gemm_auto", "gemm", "dequantize", "convert_layout", "prepack",
+    "gemm_i", "gemm_j", "gemm_k", "gemm_m", "gemm_auto", "gemm", "dequantize", "quantize", "convert_layout", "prepack",
     "select_plan", "device_info", "shape_supported_c", "shape_supported_d",
     "shape_supported_e", "shape_supported_f", "shape_supported_g", "version",
     "LAYOUT_KN", "LAYOUT_NK", "LAYOUT_G", "LAYOUT_P", "KERNEL_AUTO", "KERNEL_GEMV", "KERNEL_TILED", "KERNEL_GENERIC", "KERNEL_STREAM",

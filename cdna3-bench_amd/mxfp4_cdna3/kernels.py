@@ -12,7 +12,8 @@ Reference functions and their counterparts:
   gemm_auto         (kernels.py:63-74)  every shape with K % 32 == 0
   device_info, shape_supported_{c,d,e,f,g} (kernels.py:11-32)
 Additions: ``gemm`` (any weight layout, bf16/fp32 out, explicit plan),
-``dequantize`` (device dequant tile), ``prepack`` / ``convert_layout``
+``dequantize`` (device dequant tile), ``quantize`` (device quantize_mxfp4,
+ref.py:14-47), ``prepack`` / ``convert_layout``
 (device counterpart of ref.py:85-101 ``prepack_b_mxfp4``, between any two
 layouts), ``select_plan``.
 """
@@ -125,6 +126,15 @@ def dequantize(B, S, layout=LAYOUT_KN, out_dtype=torch.bfloat16, K=None):
     """Dequantized weights [K, N] on the device (bf16 or fp32).  K is needed
     only for flat g / p weights."""
     return _ext.dequant(B, S, layout, out_dtype, K)
+
+
+def quantize(X, axis=-1, layout=None):
+    """Device quantize_mxfp4 (ref.py:14-47) of a 2-D fp32 / bf16 tensor,
+    bit-exact with the reference for finite inputs.  axis=0: X is [K, N]
+    (returns [K/2, N], [K/32, N] by default); axis=-1: X is [N, K] (returns
+    [N, K/2], [N, K/32]).  ``layout`` asks for "kn", "nk", "g" or "p" instead.
+    """
+    return _ext.quantize(X, axis, layout)
 
 
 def convert_layout(B, S, src, dst, K=None):

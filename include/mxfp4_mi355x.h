@@ -48,6 +48,7 @@ extern "C" {
 
 enum { MXFP4_LAYOUT_KN = 0, MXFP4_LAYOUT_NK = 1, MXFP4_LAYOUT_G = 2, MXFP4_LAYOUT_P = 3 };
 enum { MXFP4_OUT_F32 = 0, MXFP4_OUT_BF16 = 1 };
+enum { MXFP4_IN_F32 = 0, MXFP4_IN_BF16 = 1 };
 enum {
   MXFP4_KERNEL_AUTO = 0,    /* cost-model choice */
   MXFP4_KERNEL_GEMV = 1,    /* memory-bound family, M <= 32 */
@@ -131,6 +132,20 @@ hipError_t mxfp4_dequant(const uint8_t* B, const uint8_t* S, void* out, int out_
 hipError_t mxfp4_convert_layout(const uint8_t* B, const uint8_t* S, int src_layout, uint8_t* B_out,
                                 uint8_t* S_out, int dst_layout, int64_t K, int64_t N,
                                 hipStream_t stream);
+
+/*
+ * Quantizes a K x N weight matrix X to MXFP4: codes B and E8M0 scales S in
+ * b_layout (any MXFP4_LAYOUT_*, its shape rules apply), one scale per 32 K.
+ * X is fp32 or bf16 (x_dtype MXFP4_IN_*), row-major [K, N] (x_layout
+ * MXFP4_LAYOUT_KN: quantize_mxfp4(X, axis=0)) or [N, K] (MXFP4_LAYOUT_NK:
+ * quantize_mxfp4(X, axis=-1)).  Device counterpart of quantize_mxfp4
+ * (python/mxfp4_cdna3/ref.py:14-47), bit-exact with it for finite inputs
+ * (argmin ties to the smaller magnitude; float32 ceil(log2(amax / 6))
+ * clipped to [-127, 127]); NaN / inf inputs give unspecified codes.  X and
+ * B 16-byte aligned.
+ */
+hipError_t mxfp4_quantize(const void* X, int x_dtype, int x_layout, int64_t K, int64_t N, uint8_t* B,
+                          uint8_t* S, int b_layout, hipStream_t stream);
 
 /*
  * The reference's shape predicates (csrc/common.h:80-99), strategy 'c'..'g'

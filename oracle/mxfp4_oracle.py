@@ -18,7 +18,8 @@ What it restates (reference = konradha/cdna3-bench):
 * bf16 round-to-nearest-even     csrc/strategy_c_dequant.h:68-73
 * E8M0 bit-cast (GPU semantics)  csrc/strategy_h_dequant.h:65-67
 
-How each function is pinned (tests/test_oracle.py):
+How each function is pinned (tests/test_oracle.py, test_layouts.py,
+test_quantize.py):
 
 * E2M1 table: closed form from the E2M1 bit fields (sign bit 3, 2 exponent
   bits with bias 1, 1 mantissa bit) and the reference KAT
@@ -39,10 +40,11 @@ How each function is pinned (tests/test_oracle.py):
   plain-Python index loops, and the C++ index functions of the device code
   (cdna3-bench_amd/csrc/mxfp4_layout.h, compiled with g++) agree with it for
   every byte of small shapes, for all four layouts.
-* ``quantize_mxfp4``: the reference's own KATs (tests/test_smoke.py:6-28).
-  Its argmin tie-breaking (first minimum, i.e. toward the smaller magnitude)
-  follows numpy's documented argmin semantics; beyond those KATs it is
-  "parity unpinned".  It only produces inputs, never checks outputs.
+* ``quantize_mxfp4``: bit-exact against input/output vectors recorded from
+  the reference's own ``quantize_mxfp4`` (tests/golden/
+  make_quantize_vectors.py, run in the build container: argmin ties,
+  exponent edges, clipping, subnormals, axis 0 and -1) and the reference's
+  KATs (tests/test_smoke.py:6-28).
 """
 
 from __future__ import annotations
