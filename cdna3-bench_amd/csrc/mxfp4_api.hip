@@ -299,14 +299,39 @@ hipError_t check_args(const void* A, const uint8_t* B, const uint8_t* S, void* C
   return hipSuccess;
 }
 
+// The kernels' view of a caller's epilogue (NULL: none).
+hipError_t make_epilogue(const mxfp4_epilogue* in, Epilogue* out) {
+  *out = Epilogue{};
+  if (!in) return hipSuccess;
+  if (in->activation < MXFP4_ACT_NONE || in->activation > MXFP4_ACT_GELU_TANH) return hipErrorInvalidValue;
+  if (in->bias_dtype != MXFP4_OUT_F32 && in->bias_dtype != MXFP4_OUT_BF16) return hipErrorInvalidValue;
+  if (in->residual_dtype != MXFP4_OUT_F32 && in->residual_dtype != MXFP4_OUT_BF16) return hipErrorInvalidValue;
+  const uintptr_t ab = in->bias_dtype == MXFP4_OUT_BF16 ? 1 : 3, ar = in->residual_dtype == MXFP4_OUT_BF16 ? 1 : 3;
+  if (((uintptr_t)in->bias & ab) || ((uintptr_t)in->residual & ar)) return hipErrorInvalidValue;
+  out->bias = in->bias;
+  out->residual = in->residual;
+  out->bias_bf16 = in->bias_dtype == MXFP4_OUT_BF16;
+  out->res_bf16 = in->residual_dtype == MXFP4_OUT_BF16;
+  out->act = in->activation;
+  out->any = in->bias != nullptr || in->residual != nullptr || in->activation != MXFP4_ACT_NONE;
+  return hipSuccess;
+}
+
 hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype, int64_t M,
-               int64_t N, int64_t K, int layout, const mxfp4_plan* plan_in, void* workspace,
-               size_t workspace_bytes, hipStream_t stream) {
+               int64_t N, int64_t K, int layout, const mxfp4_plan* plan_in, const mxfp4_epilogue* ep_in,
+               void* workspace, size_t workspace_bytes, hipStream_t stream) {
   hipError_t e = check_args(A, B, S, C, c_dtype, M, N, K, layout);
+  if (e != hipSuccess) return e;
+  Epilogue ep;
+  e = make_epilogue(ep_in, &ep);
   if (e != hipSuccess) return e;
   if (M * N == 0) return hipSuccess;
   const int out_bf16 = c_dtype == MXFP4_OUT_BF16;
-  if (K == 0) return launch_zero_fill(C, (size_t)M * N * (out_bf16 ? 2 : 4), stream);
+  if (K == 0) {
+    // C = act(0 + bias) + residual: the generic kernel with an empty K loop
+    if (ep.any) return launch_generic(layout, nullptr, B, S, C, out_bf16, (int)M, (int)N, 0, ep, stream);
+    return launch_zero_fill(C, (size_t)M * N * (out_bf16 ? 2 : 4), stream);
+  }
 
   mxfp4_plan plan;
   if (plan_in && plan_in->kernel != MXFP4_KERNEL_AUTO) {
@@ -333,7 +358,7 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
   const uint16_t* A16 = static_cast<const uint16_t*>(A);
   switch (plan.kernel) {
     case MXFP4_KERNEL_GENERIC:
-      return launch_generic(layout, A16, B, S, C, out_bf16, (int)M, (int)N, (int)K, stream);
+      return launch_generic(layout, A16, B, S, C, out_bf16, (int)M, (int)N, (int)K, ep, stream);
     case MXFP4_KERNEL_GEMV: {
       const GemvShape& g = kGemv[plan.variant];
       GemvArgs a{};
@@ -346,6 +371,7 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
       a.splits = (int)ceil_div(a.steps, a.steps_per_split);
       a.partials = a.splits > 1 ? partials : nullptr;
       a.counters = a.splits > 1 ? counters : nullptr;
+      a.ep = ep;
       return launch_gemv(layout, g, a, stream);
     }
     case MXFP4_KERNEL_STREAM: {
@@ -360,6 +386,7 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
       a.partials = a.splits > 1 ? partials : nullptr;
       a.counters = a.splits > 1 ? counters : nullptr;
       a.spin_limit = kStreamSpin;
+      a.ep = ep;
       return launch_stream(layout, s, a, stream);
     }
     case MXFP4_KERNEL_TILED: {
@@ -376,6 +403,7 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
       a.splits = (int)ceil_div(a.ksteps, a.steps_per_split);
       a.partials = a.splits > 1 ? partials : nullptr;
       a.counters = a.splits > 1 ? counters : nullptr;
+      a.ep = ep;
       return kTiled[plan.variant].pipe ? launch_tiled_pipe(layout, s, a, stream)
                                        : launch_tiled(layout, s, a, stream);
     }
@@ -449,14 +477,21 @@ size_t mxfp4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int b_layout,
 hipError_t mxfp4_gemm(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype,
                       int64_t M, int64_t N, int64_t K, int b_layout, void* workspace,
                       size_t workspace_bytes, hipStream_t stream) {
-  return run(A, B, S, C, c_dtype, M, N, K, b_layout, nullptr, workspace, workspace_bytes, stream);
+  return run(A, B, S, C, c_dtype, M, N, K, b_layout, nullptr, nullptr, workspace, workspace_bytes, stream);
 }
 
 hipError_t mxfp4_gemm_with_plan(const void* A, const uint8_t* B, const uint8_t* S, void* C,
                                 int c_dtype, int64_t M, int64_t N, int64_t K, int b_layout,
                                 const mxfp4_plan* plan, void* workspace, size_t workspace_bytes,
                                 hipStream_t stream) {
-  return run(A, B, S, C, c_dtype, M, N, K, b_layout, plan, workspace, workspace_bytes, stream);
+  return run(A, B, S, C, c_dtype, M, N, K, b_layout, plan, nullptr, workspace, workspace_bytes, stream);
+}
+
+hipError_t mxfp4_gemm_ex(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype,
+                         int64_t M, int64_t N, int64_t K, int b_layout, const mxfp4_plan* plan,
+                         const mxfp4_epilogue* ep, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
+  return run(A, B, S, C, c_dtype, M, N, K, b_layout, plan, ep, workspace, workspace_bytes, stream);
 }
 
 hipError_t mxfp4_dequant(const uint8_t* B, const uint8_t* S, void* out, int out_dtype, int64_t K,

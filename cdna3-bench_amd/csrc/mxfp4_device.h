@@ -203,4 +203,36 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return bf16_bits_rne(lo) | (bf16_bits_rne(hi) << 16);
 }
 
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+// ---- fused epilogue -----------------------------------------------------------
+// v = act(acc + bias[col]) + residual[row][col], in fp32 (the definitions of
+// torch.nn.functional.silu / gelu / gelu(approximate="tanh")).
+__device__ __forceinline__ float activate(int act, float v) {
+  switch (act) {
+    case 1:  // SiLU
+      return v / (1.0f + expf(-v));
+    case 2:  // GELU (erf)
+      return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    case 3:  // GELU (tanh)
+      return 0.5f * v * (1.0f + tanhf(0.79788456080286536f * (v + 0.044715f * v * v * v)));
+    default:
+      return v;
+  }
+}
+
+template <typename Ep>
+__device__ __forceinline__ float epilogue_value(const Ep& ep, float v, size_t row, size_t col, size_t N) {
+  if (ep.bias)
+    v += ep.bias_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(ep.bias)[col])
+                      : static_cast<const float*>(ep.bias)[col];
+  v = activate(ep.act, v);
+  if (ep.residual) {
+    const size_t o = row * N + col;
+    v += ep.res_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(ep.residual)[o])
+                     : static_cast<const float*>(ep.residual)[o];
+  }
+  return v;
+}
+
 }  // namespace mxfp4

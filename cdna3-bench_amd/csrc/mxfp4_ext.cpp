@@ -95,14 +95,51 @@ hipStream_t check_inputs(const torch::Tensor& A, const torch::Tensor& B, const t
 
 void launch(const char* name, const torch::Tensor& A, const torch::Tensor& B,
             const torch::Tensor& S, torch::Tensor& C, int64_t M, int64_t N, int64_t K, int layout,
-            const mxfp4_plan* plan, hipStream_t stream) {
+            const mxfp4_plan* plan, hipStream_t stream, const mxfp4_epilogue* ep = nullptr) {
   const size_t ws_bytes = mxfp4_gemm_workspace_bytes(M, N, K, layout, plan);
   torch::Tensor ws = workspace_for(A, ws_bytes);
-  hipError_t err = mxfp4_gemm_with_plan(A.data_ptr(), static_cast<const uint8_t*>(B.data_ptr()),
-                                        static_cast<const uint8_t*>(S.data_ptr()), C.data_ptr(),
-                                        out_code(C), M, N, K, layout, plan,
-                                        ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream);
+  hipError_t err = mxfp4_gemm_ex(A.data_ptr(), static_cast<const uint8_t*>(B.data_ptr()),
+                                 static_cast<const uint8_t*>(S.data_ptr()), C.data_ptr(), out_code(C), M, N,
+                                 K, layout, plan, ep, ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream);
   TORCH_CHECK(err == hipSuccess, name, ": ", hipGetErrorString(err));
+}
+
+int activation_code(const c10::optional<std::string>& act) {
+  if (!act.has_value() || *act == "none") return MXFP4_ACT_NONE;
+  if (*act == "silu") return MXFP4_ACT_SILU;
+  if (*act == "gelu") return MXFP4_ACT_GELU_ERF;
+  if (*act == "gelu_tanh") return MXFP4_ACT_GELU_TANH;
+  TORCH_CHECK(false, "activation must be None, 'silu', 'gelu' or 'gelu_tanh'");
+  return MXFP4_ACT_NONE;
+}
+
+// Fused epilogue arguments: bias [N], residual [M, N] (fp32 or bf16, on C's device).
+mxfp4_epilogue make_epilogue(const torch::Tensor& C, int64_t M, int64_t N, const c10::optional<torch::Tensor>& bias,
+                             const c10::optional<std::string>& activation,
+                             const c10::optional<torch::Tensor>& residual) {
+  mxfp4_epilogue ep{};
+  ep.activation = activation_code(activation);
+  auto dtype_code = [](const torch::Tensor& t, const char* what) {
+    TORCH_CHECK(t.scalar_type() == at::kFloat || t.scalar_type() == at::kBFloat16, what,
+                " must be float32 or bfloat16");
+    return t.scalar_type() == at::kBFloat16 ? MXFP4_OUT_BF16 : MXFP4_OUT_F32;
+  };
+  if (bias.has_value()) {
+    const auto& b = *bias;
+    TORCH_CHECK(b.is_cuda() && b.get_device() == C.get_device(), "bias must be on C's GPU");
+    TORCH_CHECK(b.dim() == 1 && b.size(0) == N && b.is_contiguous(), "bias must be a contiguous [N] vector");
+    ep.bias = b.data_ptr();
+    ep.bias_dtype = dtype_code(b, "bias");
+  }
+  if (residual.has_value()) {
+    const auto& r = *residual;
+    TORCH_CHECK(r.is_cuda() && r.get_device() == C.get_device(), "residual must be on C's GPU");
+    TORCH_CHECK(r.dim() == 2 && r.size(0) == M && r.size(1) == N && r.is_contiguous(),
+                "residual must be a contiguous [M, N] matrix");
+    ep.residual = r.data_ptr();
+    ep.residual_dtype = dtype_code(r, "residual");
+  }
+  return ep;
 }
 
 // Reference dispatch (csrc/mxfp4_ext.cpp:36-48): C=None -> fp32 [M, N].
@@ -164,10 +201,12 @@ torch::Tensor gemm_auto(const torch::Tensor& A, const torch::Tensor& B, const to
 // Any weight layout ("kn": [K/2,N]/[K/32,N], "nk": [N,K/2]/[N,K/32], "g":
 // the strategy-G prepack, "p": panels; g and p in any shape of the right
 // size, N = numel / (K/2)), output dtype, and an optional explicit plan
-// (kernel, variant, split_k).
+// (kernel, variant, split_k), and a fused epilogue C = act(A W + bias) + residual.
 torch::Tensor gemm(const torch::Tensor& A, const torch::Tensor& B, const torch::Tensor& S,
                    c10::optional<torch::Tensor> C_opt, const std::string& layout,
-                   c10::optional<at::ScalarType> out_dtype, c10::optional<std::vector<int64_t>> plan) {
+                   c10::optional<at::ScalarType> out_dtype, c10::optional<std::vector<int64_t>> plan,
+                   c10::optional<torch::Tensor> bias, c10::optional<std::string> activation,
+                   c10::optional<torch::Tensor> residual) {
   const int lay = layout_code(layout);
   TORCH_CHECK(A.dim() == 2 && (prepacked(lay) || B.dim() == 2), "A shape");
   const int64_t M = A.size(0), K = A.size(1);
@@ -189,7 +228,8 @@ torch::Tensor gemm(const torch::Tensor& A, const torch::Tensor& B, const torch::
     p.variant = (int32_t)(*plan)[1];
     p.split_k = (int32_t)(*plan)[2];
   }
-  launch("mxfp4_gemm", A, B, S, C, M, N, K, lay, &p, stream);
+  const mxfp4_epilogue ep = make_epilogue(C, M, N, bias, activation, residual);
+  launch("mxfp4_gemm", A, B, S, C, M, N, K, lay, &p, stream, &ep);
   return C;
 }
 
@@ -389,7 +429,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   abc("gemm_auto", &gemm_auto);
   m.def("gemm_g", &gemm_g, py::arg("A"), py::arg("B_prep"), py::arg("Bs_prep"), py::arg("C") = py::none());
   m.def("gemm", &gemm, py::arg("A"), py::arg("B"), py::arg("S"), py::arg("C") = py::none(),
-        py::arg("layout") = "kn", py::arg("out_dtype") = py::none(), py::arg("plan") = py::none());
+        py::arg("layout") = "kn", py::arg("out_dtype") = py::none(), py::arg("plan") = py::none(),
+        py::arg("bias") = py::none(), py::arg("activation") = py::none(), py::arg("residual") = py::none());
   m.def("dequant", &dequant, py::arg("B"), py::arg("S"), py::arg("layout") = "kn",
         py::arg("out_dtype") = at::kBFloat16, py::arg("K") = py::none());
   m.def("quantize", &quantize, py::arg("X"), py::arg("axis") = -1, py::arg("layout") = py::none());

@@ -245,10 +245,11 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
     for (int e = 0; e < PER; ++e) {
       const int row = row_of(e), col = n0 + col_of(ch, e);
       if (live(e) && row < M && col < N) {
+        const float x = p.ep.any ? epilogue_value(p.ep, v[ch][e], row, col, N) : v[ch][e];
         if (p.out_bf16)
-          static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(v[ch][e]);
+          static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(x);
         else
-          static_cast<float*>(p.C)[(size_t)row * N + col] = v[ch][e];
+          static_cast<float*>(p.C)[(size_t)row * N + col] = x;
       }
     }
 }

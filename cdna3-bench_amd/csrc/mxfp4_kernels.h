@@ -10,6 +10,15 @@
 
 namespace mxfp4 {
 
+// Fused epilogue of the GEMM kernels: v = act(acc + bias[col]) + residual[row][col].
+struct Epilogue {
+  const void* bias = nullptr;      // [N]
+  const void* residual = nullptr;  // [M, N]
+  int bias_bf16 = 0, res_bf16 = 0;
+  int act = 0;                     // MXFP4_ACT_*
+  int any = 0;                     // any term present (else the plain store)
+};
+
 // Tiled MFMA family (M > 32): BM x BN x 64 tiles, WM x WN waves, each wave
 // owning RB 32-row blocks x 128 columns, bf16 MFMA 32x32x16.
 struct TiledArgs {
@@ -26,6 +35,8 @@ struct TiledArgs {
   int splits;
   float* partials;      // splits > 1: [tiles][splits][BM*BN]
   uint32_t* counters;   // splits > 1: [tiles], zero on entry, zero on exit
+
+  Epilogue ep;
 };
 
 struct TiledShape {
@@ -51,6 +62,8 @@ struct GemvArgs {
   int splits;
   float* partials;      // splits > 1: [col_groups][splits][rows*cols]
   uint32_t* counters;   // splits > 1: [col_groups]
+
+  Epilogue ep;
 };
 
 struct GemvShape {
@@ -91,6 +104,8 @@ struct StreamArgs {
   float* partials;      // splits > 1: [ctas][splits][16*mt*32] packets of 8 bytes, zero on entry/exit
   uint32_t* counters;   // splits > 1: [ctas], zero on entry, zero on exit
   int spin_limit;       // polls of the late unit before it falls back to counter arbitration
+
+  Epilogue ep;
 };
 
 struct StreamShape {
@@ -110,7 +125,8 @@ bool stream_shape_available(const StreamShape& shape);
 // Any shape with K % 32 == 0; one thread per output, for shapes the fast
 // families do not cover (N % 16 != 0, unaligned pointers).
 hipError_t launch_generic(int layout, const uint16_t* A, const uint8_t* B, const uint8_t* S,
-                          void* C, int out_bf16, int M, int N, int K, hipStream_t stream);
+                          void* C, int out_bf16, int M, int N, int K, const Epilogue& ep,
+                          hipStream_t stream);
 
 // Dequantized [K, N] tile (bf16 or fp32) from either layout.
 hipError_t launch_dequant(int layout, const uint8_t* B, const uint8_t* S, void* out,

@@ -43,7 +43,7 @@ template <int LAYOUT>
 __global__ void __launch_bounds__(256) generic_kernel(const uint16_t* __restrict__ A,
                                                       const uint8_t* __restrict__ B,
                                                       const uint8_t* __restrict__ S, void* C,
-                                                      int out_bf16, int M, int N, int K) {
+                                                      int out_bf16, int M, int N, int K, Epilogue ep) {
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (size_t)M * N) return;
   const int m = (int)(idx / N), n = (int)(idx - (size_t)m * N);
@@ -57,6 +57,7 @@ __global__ void __launch_bounds__(256) generic_kernel(const uint16_t* __restrict
     acc = __builtin_fmaf(a0, __builtin_bit_cast(float, w << 16), acc);
     acc = __builtin_fmaf(a1, __builtin_bit_cast(float, w & 0xFFFF0000u), acc);
   }
+  if (ep.any) acc = epilogue_value(ep, acc, m, n, N);
   if (out_bf16)
     static_cast<uint16_t*>(C)[idx] = (uint16_t)bf16_bits_rne(acc);
   else
@@ -159,10 +160,10 @@ struct DequantLaunch {
 template <int L>
 struct GenericLaunch {
   static hipError_t run(const uint16_t* A, const uint8_t* B, const uint8_t* S, void* C, int out_bf16,
-                        int M, int N, int K, hipStream_t stream) {
+                        int M, int N, int K, Epilogue ep, hipStream_t stream) {
     const size_t total = (size_t)M * N;
     hipLaunchKernelGGL(generic_kernel<L>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
-                       A, B, S, C, out_bf16, M, N, K);
+                       A, B, S, C, out_bf16, M, N, K, ep);
     return hipGetLastError();
   }
 };
@@ -202,9 +203,10 @@ hipError_t launch_dequant(int layout, const uint8_t* B, const uint8_t* S, void* 
 }
 
 hipError_t launch_generic(int layout, const uint16_t* A, const uint8_t* B, const uint8_t* S,
-                          void* C, int out_bf16, int M, int N, int K, hipStream_t stream) {
+                          void* C, int out_bf16, int M, int N, int K, const Epilogue& ep,
+                          hipStream_t stream) {
   if ((size_t)M * N == 0) return hipSuccess;
-  return by_layout<GenericLaunch>(layout, A, B, S, C, out_bf16, M, N, K, stream);
+  return by_layout<GenericLaunch>(layout, A, B, S, C, out_bf16, M, N, K, ep, stream);
 }
 
 hipError_t launch_convert(int src_layout, int dst_layout, const uint8_t* B, const uint8_t* S,

@@ -353,10 +353,11 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (col + i >= N) break;
+      const float y = p.ep.any ? epilogue_value(p.ep, x[i], row, col + i, N) : x[i];
       if (p.out_bf16)
-        static_cast<uint16_t*>(p.C)[(size_t)row * N + col + i] = (uint16_t)bf16_bits_rne(x[i]);
+        static_cast<uint16_t*>(p.C)[(size_t)row * N + col + i] = (uint16_t)bf16_bits_rne(y);
       else
-        static_cast<float*>(p.C)[(size_t)row * N + col + i] = x[i];
+        static_cast<float*>(p.C)[(size_t)row * N + col + i] = y;
     }
   };
   auto clear_packets = [&](int g, int rs) {

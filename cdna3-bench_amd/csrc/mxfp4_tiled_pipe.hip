@@ -473,22 +473,23 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
       if constexpr (kColumnWords<LAYOUT>) {
         const int col = n0 + wn * WCOLS + WNC * c;
         if (col >= N) continue;
+        float v[WNC];
+#pragma unroll
+        for (int j = 0; j < WNC; ++j)
+          v[j] = p.ep.any ? epilogue_value(p.ep, acc[rb][j][i], row, col + j, N) : acc[rb][j][i];
         if constexpr (WNC == 4) {
           if (p.out_bf16) {
-            u32x2 v = {pack_bf16x2(acc[rb][0][i], acc[rb][1][i]), pack_bf16x2(acc[rb][2][i], acc[rb][3][i])};
-            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = v;
+            u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = w;
           } else {
-            f32x4 v = {acc[rb][0][i], acc[rb][1][i], acc[rb][2][i], acc[rb][3][i]};
-            *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col) = v;
+            *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col) = f32x4{v[0], v[1], v[2], v[3]};
           }
         } else {
           if (p.out_bf16) {
-            *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) =
-                pack_bf16x2(acc[rb][0][i], acc[rb][1][i]);
+            *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = pack_bf16x2(v[0], v[1]);
           } else {
             typedef float f32x2 __attribute__((ext_vector_type(2)));
-            *reinterpret_cast<f32x2*>(static_cast<float*>(p.C) + (size_t)row * N + col) =
-                f32x2{acc[rb][0][i], acc[rb][1][i]};
+            *reinterpret_cast<f32x2*>(static_cast<float*>(p.C) + (size_t)row * N + col) = f32x2{v[0], v[1]};
           }
         }
       } else {
@@ -496,10 +497,11 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
         for (int cb = 0; cb < WNC; ++cb) {
           const int col = n0 + wn * WCOLS + 32 * cb + c;
           if (col >= N) continue;
+          const float v = p.ep.any ? epilogue_value(p.ep, acc[rb][cb][i], row, col, N) : acc[rb][cb][i];
           if (p.out_bf16)
-            static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(acc[rb][cb][i]);
+            static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(v);
           else
-            static_cast<float*>(p.C)[(size_t)row * N + col] = acc[rb][cb][i];
+            static_cast<float*>(p.C)[(size_t)row * N + col] = v;
         }
       }
     }

@@ -112,14 +112,19 @@ def gemm_auto(A, B_packed, B_scales, C=None):
     return _ext.gemm_auto(A, B_packed, B_scales, C)
 
 
-def gemm(A, B, S, C=None, layout=LAYOUT_KN, out_dtype=None, plan=None):
-    """C = A @ dequant(B, S) in any weight layout (g / p: any shape of the
-    layout's size, N = B.numel() / (K/2)).
+def gemm(A, B, S, C=None, layout=LAYOUT_KN, out_dtype=None, plan=None, bias=None, activation=None,
+         residual=None):
+    """C = act(A @ dequant(B, S) + bias) + residual in any weight layout (g / p:
+    any shape of the layout's size, N = B.numel() / (K/2)).
 
     out_dtype: torch.float32 (default) or torch.bfloat16 when C is None.
     plan: optional (kernel, variant, split_k) overriding the cost model.
+    bias [N], residual [M, N] (fp32 or bf16; residual may be C itself) and
+    activation (None, "silu", "gelu", "gelu_tanh") are fused into the
+    kernel's store, in fp32 before the rounding to C's dtype.
     """
-    return _ext.gemm(A, B, S, C, layout, out_dtype, None if plan is None else list(plan))
+    return _ext.gemm(A, B, S, C, layout, out_dtype, None if plan is None else list(plan), bias, activation,
+                     residual)
 
 
 def dequantize(B, S, layout=LAYOUT_KN, out_dtype=torch.bfloat16, K=None):

@@ -49,6 +49,7 @@ extern "C" {
 enum { MXFP4_LAYOUT_KN = 0, MXFP4_LAYOUT_NK = 1, MXFP4_LAYOUT_G = 2, MXFP4_LAYOUT_P = 3 };
 enum { MXFP4_OUT_F32 = 0, MXFP4_OUT_BF16 = 1 };
 enum { MXFP4_IN_F32 = 0, MXFP4_IN_BF16 = 1 };
+enum { MXFP4_ACT_NONE = 0, MXFP4_ACT_SILU = 1, MXFP4_ACT_GELU_ERF = 2, MXFP4_ACT_GELU_TANH = 3 };
 enum {
   MXFP4_KERNEL_AUTO = 0,    /* cost-model choice */
   MXFP4_KERNEL_GEMV = 1,    /* memory-bound family, M <= 32 */
@@ -64,6 +65,23 @@ typedef struct mxfp4_plan {
   int32_t split_k; /* >= 1 */
   int32_t reserved;
 } mxfp4_plan;
+
+/*
+ * Fused epilogue: C = act(A x W + bias) + residual, in fp32, then rounded to
+ * C's dtype.  act: SiLU x / (1 + e^-x); GELU 0.5 x (1 + erf(x / sqrt 2));
+ * GELU-tanh 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) -- the
+ * definitions of torch.nn.functional.silu / gelu.  bias: [N]; residual:
+ * [M, N] row-major, may be C itself (each element is read before it is
+ * written by the same thread).  NULL pointers skip the term.
+ */
+typedef struct mxfp4_epilogue {
+  const void* bias;       /* [N] or NULL */
+  const void* residual;   /* [M, N] or NULL */
+  int32_t bias_dtype;     /* MXFP4_OUT_F32 or MXFP4_OUT_BF16 */
+  int32_t residual_dtype; /* MXFP4_OUT_F32 or MXFP4_OUT_BF16 */
+  int32_t activation;     /* MXFP4_ACT_* */
+  int32_t reserved;       /* 0 */
+} mxfp4_epilogue;
 
 /* Device properties; replaces device_info (csrc/mxfp4_ext.cpp:156-168). */
 typedef struct mxfp4_device_info_t {
@@ -110,6 +128,17 @@ hipError_t mxfp4_gemm_with_plan(const void* A, const uint8_t* B, const uint8_t* 
                                 int c_dtype, int64_t M, int64_t N, int64_t K, int b_layout,
                                 const mxfp4_plan* plan, void* workspace, size_t workspace_bytes,
                                 hipStream_t stream);
+
+/*
+ * mxfp4_gemm_with_plan with a fused epilogue (ep NULL = none; plan NULL =
+ * the auto plan).  No counterpart in the reference, whose kernels end in a
+ * plain fp32 store (csrc/bf16_gemm.h:136-153); it replaces the separate
+ * bias / activation / residual passes a caller would run over C.
+ */
+hipError_t mxfp4_gemm_ex(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype,
+                         int64_t M, int64_t N, int64_t K, int b_layout, const mxfp4_plan* plan,
+                         const mxfp4_epilogue* ep, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
 
 /*
  * out[K, N] = dequant(B, S) as bf16 (out_dtype MXFP4_OUT_BF16) or fp32.
