@@ -23,32 +23,38 @@ constexpr double kHbmBytesPerS = 8.0e12;
 constexpr double kMfmaFlopsPerS = 2.5e15;
 constexpr double kLaunchS = 2.0e-6;  // fixed per-launch cost folded into every plan
 
+// Tiled kernel families: the first version (mxfp4_tiled.hip), the pipelined
+// kernel (mxfp4_tiled_pipe.hip) and the hand-scheduled 256 x 256 kernel
+// (mxfp4_tiled_sched.hip, [K/2,N] weights, K % 64 == 0).
+constexpr int kFamilyPlain = 0, kFamilyPipe = 1, kFamilySched = 2;
+
 struct TiledVariant {
   TiledShape shape;
   double eff_kn, eff_nk;  // sustained fraction of the 2.5 PF/s peak, per weight layout (measured)
   int ctas_per_cu;        // residency (registers / LDS)
-  bool pipe;              // pipelined kernel (mxfp4_tiled_pipe.hip)
+  int family;             // kFamily*: which tiled kernel runs the shape
 };
 
 // Tile variants of the tiled family; index = mxfp4_plan.variant.  The
 // efficiencies are calibrated on MI355X with seeded random data (A ~ N(0,1),
 // uniform E2M1 codes), where power limits the MFMA rate well below peak.
 const TiledVariant kTiled[] = {
-    {{2, 2, 4}, 0.35, 0.31, 1, false},        // 0: 256 x 256, 4 waves, 128 x 128 per wave
-    {{4, 2, 2}, 0.42, 0.33, 1, false},        // 1: 256 x 256, 8 waves
-    {{2, 2, 2}, 0.28, 0.23, 2, false},        // 2: 128 x 256
-    {{1, 2, 2}, 0.30, 0.26, 2, false},        // 3:  64 x 256
-    {{2, 1, 2}, 0.26, 0.27, 2, false},        // 4: 128 x 128
-    {{1, 2, 1}, 0.20, 0.17, 4, false},        // 5:  32 x 256
-    {{4, 2, 2, 4, 3}, 0.433, 0.336, 1, true}, // 6: pipelined 256 x 256, 8 waves of 64 x 128, 3 stages
-    {{2, 2, 2, 4, 3}, 0.32, 0.23, 1, true},   // 7: pipelined 128 x 256, 4 waves of 64 x 128
-    {{4, 2, 2, 4, 3}, 0.432, 0.333, 1, true}, // 8: = 6 (a 4-stage 256 x 256 ring no longer fits 160 KB)
-    {{2, 4, 4, 2, 3}, 0.37, 0.361, 1, true},  // 9: = 10
-    {{2, 4, 4, 2, 3}, 0.37, 0.361, 1, true},  // 10: as 9 with 3 stages
-    {{2, 2, 2, 4, 4}, 0.33, 0.23, 1, true},   // 11: as 7 with 4 stages
-    {{2, 4, 2, 2, 4}, 0.31, 0.26, 1, true},   // 12: pipelined 128 x 256, 8 waves of 64 x 64
-    {{1, 4, 4, 2, 4}, 0.32, 0.25, 1, true},   // 13: pipelined 128 x 256, 4 waves of 128 x 64
-    {{2, 1, 2, 4, 4}, 0.28, 0.24, 2, true},   // 14: pipelined 128 x 128, 2 waves
+    {{2, 2, 4}, 0.35, 0.31, 1, kFamilyPlain},       // 0: 256 x 256, 4 waves, 128 x 128 per wave
+    {{4, 2, 2}, 0.42, 0.33, 1, kFamilyPlain},       // 1: 256 x 256, 8 waves
+    {{2, 2, 2}, 0.28, 0.23, 2, kFamilyPlain},       // 2: 128 x 256
+    {{1, 2, 2}, 0.30, 0.26, 2, kFamilyPlain},       // 3:  64 x 256
+    {{2, 1, 2}, 0.26, 0.27, 2, kFamilyPlain},       // 4: 128 x 128
+    {{1, 2, 1}, 0.20, 0.17, 4, kFamilyPlain},       // 5:  32 x 256
+    {{4, 2, 2, 4, 3}, 0.433, 0.336, 1, kFamilyPipe},// 6: pipelined 256 x 256, 8 waves of 64 x 128, 3 stages
+    {{2, 2, 2, 4, 3}, 0.32, 0.23, 1, kFamilyPipe},  // 7: pipelined 128 x 256, 4 waves of 64 x 128
+    {{4, 2, 2, 4, 3}, 0.432, 0.333, 1, kFamilyPipe},// 8: = 6 (a 4-stage 256 x 256 ring no longer fits 160 KB)
+    {{2, 4, 4, 2, 3}, 0.37, 0.361, 1, kFamilyPipe}, // 9: = 10
+    {{2, 4, 4, 2, 3}, 0.37, 0.361, 1, kFamilyPipe}, // 10: as 9 with 3 stages
+    {{2, 2, 2, 4, 4}, 0.33, 0.23, 1, kFamilyPipe},  // 11: as 7 with 4 stages
+    {{2, 4, 2, 2, 4}, 0.31, 0.26, 1, kFamilyPipe},  // 12: pipelined 128 x 256, 8 waves of 64 x 64
+    {{1, 4, 4, 2, 4}, 0.32, 0.25, 1, kFamilyPipe},  // 13: pipelined 128 x 256, 4 waves of 128 x 64
+    {{2, 1, 2, 4, 4}, 0.28, 0.24, 2, kFamilyPipe},  // 14: pipelined 128 x 128, 2 waves
+    {{2, 2, 2, 4, 3}, 0.0, 0.0, 2, kFamilySched},  // 15: hand-scheduled 128 x 256, 4 waves of 64 x 128, 2 CTAs / CU
 };
 constexpr int kNumTiled = sizeof(kTiled) / sizeof(kTiled[0]);
 
@@ -163,7 +169,8 @@ double tiled_eff(const TiledVariant& v, int layout) {
 // Tiled variants a layout may use: the prepacked layouts only have loaders
 // in the pipelined kernel, whose [N,K/2] loader reads aligned scale dwords.
 bool tiled_variant_ok(const TiledVariant& v, int layout, int64_t K) {
-  if (!v.pipe) return layout == kLayoutKN || layout == kLayoutNK;
+  if (v.family == kFamilyPlain) return layout == kLayoutKN || layout == kLayoutNK;
+  if (v.family == kFamilySched) return K % 64 == 0 && tiled_sched_available(layout, v.shape);
   if (layout == kLayoutNK) return K % 128 == 0;
   if (layout == kLayoutG) return v.shape.bn() % kGCols == 0;
   return true;
@@ -404,8 +411,11 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
       a.partials = a.splits > 1 ? partials : nullptr;
       a.counters = a.splits > 1 ? counters : nullptr;
       a.ep = ep;
-      return kTiled[plan.variant].pipe ? launch_tiled_pipe(layout, s, a, stream)
-                                       : launch_tiled(layout, s, a, stream);
+      switch (kTiled[plan.variant].family) {
+        case kFamilySched: return launch_tiled_sched(layout, s, a, stream);
+        case kFamilyPipe: return launch_tiled_pipe(layout, s, a, stream);
+        default: return launch_tiled(layout, s, a, stream);
+      }
     }
     default:
       return hipErrorInvalidValue;
@@ -448,7 +458,10 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
     case MXFP4_KERNEL_TILED: {
       if (plan->variant < 0 || plan->variant >= kNumTiled) return hipErrorInvalidValue;
       const TiledShape& s = kTiled[plan->variant].shape;
-      if (kTiled[plan->variant].pipe)
+      if (kTiled[plan->variant].family == kFamilySched)
+        snprintf(buf, buf_len, "tiled-sched %dx%d w%dx%d ns%d split%d", s.bm(), s.bn(), s.wm, s.wn,
+                 s.stages, plan->split_k);
+      else if (kTiled[plan->variant].family == kFamilyPipe)
         snprintf(buf, buf_len, "tiled-pipe %dx%d w%dx%d ns%d split%d", s.bm(), s.bn(), s.wm, s.wn,
                  s.stages, plan->split_k);
       else

@@ -221,6 +221,25 @@ __device__ __forceinline__ float activate(int act, float v) {
   }
 }
 
+// Store loops.  A GEMM kernel's store loop is unrolled over every accumulator
+// element (128-256 per thread); with the epilogue's math (expf / erff / tanhf)
+// inlined per element, one loop is ~25k instructions, and walking it thrashes
+// the instruction cache: a 128 x 256 tile's plain bf16 store took 32 us when
+// the plain and fused stores shared one loop with a per-element branch.  So
+// each kernel writes its loop once, as a lambda over these tags, and calls it
+// in separate branches chosen once per thread: the plain stores (OutKind 0 =
+// fp32, 1 = bf16) are compact loops that never touch the epilogue code; the
+// fused store (StoreKind<true>) is one loop that picks the output type per
+// store (OutKind 2).
+template <bool F>
+struct StoreKind {
+  static constexpr bool value = F;
+};
+template <int V>
+struct OutKind {
+  static constexpr int value = V;
+};
+
 template <typename Ep>
 __device__ __forceinline__ float epilogue_value(const Ep& ep, float v, size_t row, size_t col, size_t N) {
   if (ep.bias)

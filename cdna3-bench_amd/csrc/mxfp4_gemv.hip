@@ -104,7 +104,7 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
 
   using Regs = GemvRegs<LAYOUT, MT, CB>;
 
-  auto load = [&](Regs& r, int st, bool live) {
+  auto load = [&](Regs& r, int st, bool live) __attribute__((always_inline)) {
     if constexpr (LAYOUT == kLayoutKN) {
       const int col = n0 + c * CB;
       const bool cok = live && col < N;
@@ -141,7 +141,7 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
     }
   };
 
-  auto compute = [&](const Regs& r) {
+  auto compute = [&](const Regs& r) __attribute__((always_inline)) {
     if constexpr (LAYOUT == kLayoutKN) {
 #pragma unroll
       for (int j = 0; j < CB; ++j) {
@@ -213,9 +213,9 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
   }
 
   // element (ch, e) <-> tile row / column
-  auto row_of = [&](int e) { return (e * NT + (int)threadIdx.x) / CCOLS; };
-  auto col_of = [&](int ch, int e) { return ch * CCOLS + (e * NT + (int)threadIdx.x) % CCOLS; };
-  auto live = [&](int e) { return (CTILE % NT == 0 || e * NT + (int)threadIdx.x < CTILE); };
+  auto row_of = [&](int e) __attribute__((always_inline)) { return (e * NT + (int)threadIdx.x) / CCOLS; };
+  auto col_of = [&](int ch, int e) __attribute__((always_inline)) { return ch * CCOLS + (e * NT + (int)threadIdx.x) % CCOLS; };
+  auto live = [&](int e) __attribute__((always_inline)) { return (CTILE % NT == 0 || e * NT + (int)threadIdx.x < CTILE); };
 
   if (p.splits > 1) {
     const __amdgpu_buffer_rsrc_t rp =
@@ -239,19 +239,30 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
       }
   }
 
+  // plain and fused stores are separate loops, chosen once (see StoreKind)
+  auto store = [&](auto fused, auto out) __attribute__((always_inline)) {
+    constexpr bool kFused = decltype(fused)::value;
+    const bool bf16 = decltype(out)::value == 2 ? p.out_bf16 != 0 : decltype(out)::value == 1;
 #pragma unroll
-  for (int ch = 0; ch < CHUNKS; ++ch)
+    for (int ch = 0; ch < CHUNKS; ++ch)
 #pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const int row = row_of(e), col = n0 + col_of(ch, e);
-      if (live(e) && row < M && col < N) {
-        const float x = p.ep.any ? epilogue_value(p.ep, v[ch][e], row, col, N) : v[ch][e];
-        if (p.out_bf16)
-          static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(x);
-        else
-          static_cast<float*>(p.C)[(size_t)row * N + col] = x;
+      for (int e = 0; e < PER; ++e) {
+        const int row = row_of(e), col = n0 + col_of(ch, e);
+        if (live(e) && row < M && col < N) {
+          const float x = kFused ? epilogue_value(p.ep, v[ch][e], row, col, N) : v[ch][e];
+          if (bf16)
+            static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(x);
+          else
+            static_cast<float*>(p.C)[(size_t)row * N + col] = x;
+        }
       }
-    }
+  };
+  if (p.ep.any)
+    store(StoreKind<true>{}, OutKind<2>{});
+  else if (p.out_bf16)
+    store(StoreKind<false>{}, OutKind<1>{});
+  else
+    store(StoreKind<false>{}, OutKind<0>{});
 }
 
 template <int LAYOUT, int MT, int CB, int WPC, int U>

@@ -83,6 +83,11 @@ hipError_t launch_tiled_pipe(int layout, const TiledShape& shape, const TiledArg
                              hipStream_t stream);
 bool tiled_pipe_shape_available(int layout, const TiledShape& shape);
 
+// Hand-scheduled 256 x 256 x 64 kernel, 4 waves of 128 x 128 ([K/2,N], K % 64 == 0).
+hipError_t launch_tiled_sched(int layout, const TiledShape& shape, const TiledArgs& args,
+                              hipStream_t stream);
+bool tiled_sched_available(int layout, const TiledShape& shape);
+
 hipError_t launch_gemv(int layout, const GemvShape& shape, const GemvArgs& args,
                        hipStream_t stream);
 bool gemv_shape_available(int layout, const GemvShape& shape);

@@ -135,7 +135,7 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
   const int jg = (int)blockIdx.x / S;
   const int M = p.M, N = p.N, K = p.K;
   const int Kh = K >> 1, G = K >> 5;
-  auto group_of = [&](int u) { return jg * S + (u + r) % S; };
+  auto group_of = [&](int u) __attribute__((always_inline)) { return jg * S + (u + r) % S; };
 
   // The compiler may lay the two roles out as sequential regions (the
   // reducer's exit falling into the compute region's guard); its wait
@@ -153,7 +153,7 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
     // DMA of unit u (< S) into ring slot u % NSLOT (lanes past the last group /
     // column / K masked).  Units past S are not issued; the waits below count
     // exactly the units in flight.
-    auto issue_unit = [&](int u) {
+    auto issue_unit = [&](int u) __attribute__((always_inline)) {
       const int sl = u % NSLOT;
       const int g = group_of(u);
       const bool live = g < p.groups;
@@ -340,13 +340,13 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
   const __amdgpu_buffer_rsrc_t pr = make_rsrc(p.partials);
   uint32_t* const cnt = p.counters;
   const bool split = S > 1;
-  auto packet_off = [&](int g, int rs, int v) {  // byte offset of element 4*lane + 256*v
+  auto packet_off = [&](int g, int rs, int v) __attribute__((always_inline)) {  // byte offset of element 4*lane + 256*v
     return (uint32_t)((((size_t)g * S + rs) * TILE + 4 * lane + 256 * v) * 8);
   };
   // The split of group g whose unit is its late unit: group t = g % S of a
   // block is processed last by the CTA with split (t + 1) % S.
-  auto late_split = [&](int g) { return (g % S + 1) % S; };
-  auto store_c = [&](int g, int v, f32x4 x) {
+  auto late_split = [&](int g) __attribute__((always_inline)) { return (g % S + 1) % S; };
+  auto store_c = [&](int g, int v, f32x4 x) __attribute__((always_inline)) {
     const int e = 4 * lane + 256 * v;
     const int row = e / GC, col = g * GC + e % GC;
     if (row >= M) return;
@@ -360,7 +360,7 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
         static_cast<float*>(p.C)[(size_t)row * N + col + i] = y;
     }
   };
-  auto clear_packets = [&](int g, int rs) {
+  auto clear_packets = [&](int g, int rs) __attribute__((always_inline)) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, pr, packet_off(g, rs, v), 0, kCPolDevice);
@@ -373,7 +373,7 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
   // every split has arrived, so their stores are in flight).  Returns false on
   // a timeout.
   constexpr int PCH = 4 / NV;  // splits per poll round: 8 VGPRs per split and row tile
-  auto sum_packets = [&](int g, int skip, int limit, f32x4 (&tot)[NV]) -> bool {
+  auto sum_packets = [&](int g, int skip, int limit, f32x4 (&tot)[NV]) __attribute__((always_inline)) -> bool {
     bool first = true;
     for (int base = 0; base < S; base += PCH) {
       u32x4 pk[PCH][NV][2];
@@ -422,7 +422,7 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
   // Reduction by the last arriver (only when a late unit gave up polling):
   // the same order as the late unit's fast path -- the other splits in
   // split order, then the late split.
-  auto reduce_from_packets = [&](int g) {
+  auto reduce_from_packets = [&](int g) __attribute__((always_inline)) {
     const int rl = late_split(g);
     f32x4 tot[NV], own[NV];
     sum_packets(g, rl, -1, tot);
@@ -449,7 +449,7 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
     for (int rs = 0; rs < S; ++rs) clear_packets(g, rs);
     if (lane == 0) __hip_atomic_store(cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
-  auto arrive = [&](int g) -> uint32_t {
+  auto arrive = [&](int g) __attribute__((always_inline)) -> uint32_t {
     uint32_t prev = 0;
     if (lane == 0) prev = __hip_atomic_fetch_add(cnt + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return prev;  // lane 0 only; read with readfirstlane once needed

@@ -94,7 +94,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_kernel(TiledArgs p) {
   const int s_end = min(p.ksteps, s_begin + p.steps_per_split);
 
   // ---- loaders -------------------------------------------------------------
-  auto load_stage = [&](int buf, int step) {
+  auto load_stage = [&](int buf, int step) __attribute__((always_inline)) {
     uint8_t* sA = smem + buf * Cfg::STAGE;
     uint8_t* sB = sA + Cfg::A_BYTES;
     const int k0 = step * kBK;
@@ -133,7 +133,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_kernel(TiledArgs p) {
   // Scales for one stage into registers: [K/32,N]: 2 words (4 columns, groups
   // g0, g0+1); [N,K/32]: 4 bytes (column block cb, group g0 + h).
   uint32_t sc_next[4] = {0u, 0u, 0u, 0u};
-  auto load_scales = [&](int step) {
+  auto load_scales = [&](int step) __attribute__((always_inline)) {
     const int g0 = step * 2;
     if constexpr (LAYOUT == kLayoutKN) {
       const int col = n0 + wn * 128 + 4 * c;
@@ -160,7 +160,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_kernel(TiledArgs p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[rb][j][e] = 0.f;
 
-  auto compute_stage = [&](int buf, const uint32_t (&sc)[4]) {
+  auto compute_stage = [&](int buf, const uint32_t (&sc)[4]) __attribute__((always_inline)) {
     const uint8_t* sA = smem + buf * Cfg::STAGE;
     const uint8_t* sB = sA + Cfg::A_BYTES;
     if constexpr (LAYOUT == kLayoutKN) {
@@ -281,39 +281,50 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_kernel(TiledArgs p) {
   }
 
   // ---- epilogue ------------------------------------------------------------
+  // Plain and fused stores are separate loops, chosen once (see StoreKind).
+  auto store = [&](auto fused, auto out) __attribute__((always_inline)) {
+    constexpr bool kFused = decltype(fused)::value;
+    const bool bf16 = decltype(out)::value == 2 ? p.out_bf16 != 0 : decltype(out)::value == 1;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int row = m0 + wm * RB * 32 + rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-      if (row >= M) continue;
-      if constexpr (LAYOUT == kLayoutKN) {
-        const int col = n0 + wn * 128 + 4 * c;
-        if (col >= N) continue;
-        float v[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          v[j] = p.ep.any ? epilogue_value(p.ep, acc[rb][j][i], row, col + j, N) : acc[rb][j][i];
-        if (p.out_bf16) {
-          u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = w;
-        } else {
-          *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col) = f32x4{v[0], v[1], v[2], v[3]};
-        }
-      } else {
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-          const int col = n0 + wn * 128 + 32 * cb + c;
+      for (int i = 0; i < 16; ++i) {
+        const int row = m0 + wm * RB * 32 + rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        if (row >= M) continue;
+        if constexpr (LAYOUT == kLayoutKN) {
+          const int col = n0 + wn * 128 + 4 * c;
           if (col >= N) continue;
-          const float v = p.ep.any ? epilogue_value(p.ep, acc[rb][cb][i], row, col, N) : acc[rb][cb][i];
-          if (p.out_bf16)
-            static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(v);
-          else
-            static_cast<float*>(p.C)[(size_t)row * N + col] = v;
+          float v[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            v[j] = kFused ? epilogue_value(p.ep, acc[rb][j][i], row, col + j, N) : acc[rb][j][i];
+          if (bf16) {
+            u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = w;
+          } else {
+            *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col) = f32x4{v[0], v[1], v[2], v[3]};
+          }
+        } else {
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb) {
+            const int col = n0 + wn * 128 + 32 * cb + c;
+            if (col >= N) continue;
+            const float v = kFused ? epilogue_value(p.ep, acc[rb][cb][i], row, col, N) : acc[rb][cb][i];
+            if (bf16)
+              static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(v);
+            else
+              static_cast<float*>(p.C)[(size_t)row * N + col] = v;
+          }
         }
       }
     }
-  }
+  };
+  if (p.ep.any)
+    store(StoreKind<true>{}, OutKind<2>{});
+  else if (p.out_bf16)
+    store(StoreKind<false>{}, OutKind<1>{});
+  else
+    store(StoreKind<false>{}, OutKind<0>{});
 }
 
 template <int LAYOUT, int WM, int WN, int RB>

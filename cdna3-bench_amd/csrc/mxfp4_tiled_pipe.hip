@@ -139,7 +139,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
   const int T = min(p.ksteps, s_begin + p.steps_per_split) - s_begin;
 
   // ---- global -> LDS ---------------------------------------------------------
-  auto load_stage = [&](int buf, int step, bool live) {
+  auto load_stage = [&](int buf, int step, bool live) __attribute__((always_inline)) {
     uint8_t* sA = smem + buf * Cfg::STAGE;
     uint8_t* sB = sA + Cfg::A_BYTES;
     const int k0 = step * kBK;
@@ -262,7 +262,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
 
   // ---- LDS -> registers ------------------------------------------------------
   using Ops = SubOps<LAYOUT, RB, WNC>;
-  auto read_ops = [&](int buf, int ks, Ops& o) {
+  auto read_ops = [&](int buf, int ks, Ops& o) __attribute__((always_inline)) {
     const uint8_t* base = smem + buf * Cfg::STAGE;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
@@ -295,7 +295,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
   };
   // [N,K/2], P: the column blocks' 16 bytes for the whole stage (column
   // blocks are 1 KB apart in both LDS images).
-  auto read_braw = [&](int buf, u32x4 (&raw)[WNC]) {
+  auto read_braw = [&](int buf, u32x4 (&raw)[WNC]) __attribute__((always_inline)) {
     const uint8_t* base = smem + buf * Cfg::STAGE + b_off;
 #pragma unroll
     for (int cb = 0; cb < WNC; ++cb) raw[cb] = *reinterpret_cast<const u32x4*>(base + cb * 1024);
@@ -310,7 +310,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
       for (int e = 0; e < 16; ++e) acc[rb][j][e] = 0.f;
 
   // cvt + MFMA for one sub-step; sc = the column scales of its K group.
-  auto mma_kn = [&](const Ops& o, const float (&sc)[WNC]) {
+  auto mma_kn = [&](const Ops& o, const float (&sc)[WNC]) __attribute__((always_inline)) {
     if constexpr (LAYOUT == kLayoutG) {
 #pragma unroll
       for (int j = 0; j < WNC; ++j) {
@@ -352,7 +352,7 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
       for (int rb = 0; rb < RB; ++rb) acc[rb][1] = mfma_32x32x16(o.a[rb], b1, acc[rb][1]);
     }
   };
-  auto mma_nk = [&](const Ops& o, const u32x4 (&raw)[WNC], const float (&sf)[WNC], int s) {
+  auto mma_nk = [&](const Ops& o, const u32x4 (&raw)[WNC], const float (&sf)[WNC], int s) __attribute__((always_inline)) {
 #pragma unroll
     for (int cb = 0; cb < WNC; ++cb) {
       const bf16x8 b = operand_from_word(raw[cb][s], sf[cb]);
@@ -464,48 +464,59 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
   }
 
   // ---- epilogue ----------------------------------------------------------------
+  // Plain and fused stores are separate loops, chosen once (see StoreKind).
+  auto store = [&](auto fused, auto out) __attribute__((always_inline)) {
+    constexpr bool kFused = decltype(fused)::value;
+    const bool bf16 = decltype(out)::value == 2 ? p.out_bf16 != 0 : decltype(out)::value == 1;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int row = m0 + wm * RB * 32 + rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-      if (row >= M) continue;
-      if constexpr (kColumnWords<LAYOUT>) {
-        const int col = n0 + wn * WCOLS + WNC * c;
-        if (col >= N) continue;
-        float v[WNC];
+      for (int i = 0; i < 16; ++i) {
+        const int row = m0 + wm * RB * 32 + rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        if (row >= M) continue;
+        if constexpr (kColumnWords<LAYOUT>) {
+          const int col = n0 + wn * WCOLS + WNC * c;
+          if (col >= N) continue;
+          float v[WNC];
 #pragma unroll
-        for (int j = 0; j < WNC; ++j)
-          v[j] = p.ep.any ? epilogue_value(p.ep, acc[rb][j][i], row, col + j, N) : acc[rb][j][i];
-        if constexpr (WNC == 4) {
-          if (p.out_bf16) {
-            u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = w;
+          for (int j = 0; j < WNC; ++j)
+            v[j] = kFused ? epilogue_value(p.ep, acc[rb][j][i], row, col + j, N) : acc[rb][j][i];
+          if constexpr (WNC == 4) {
+            if (bf16) {
+              u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+              *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = w;
+            } else {
+              *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col) = f32x4{v[0], v[1], v[2], v[3]};
+            }
           } else {
-            *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col) = f32x4{v[0], v[1], v[2], v[3]};
+            if (bf16) {
+              *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = pack_bf16x2(v[0], v[1]);
+            } else {
+              typedef float f32x2 __attribute__((ext_vector_type(2)));
+              *reinterpret_cast<f32x2*>(static_cast<float*>(p.C) + (size_t)row * N + col) = f32x2{v[0], v[1]};
+            }
           }
         } else {
-          if (p.out_bf16) {
-            *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = pack_bf16x2(v[0], v[1]);
-          } else {
-            typedef float f32x2 __attribute__((ext_vector_type(2)));
-            *reinterpret_cast<f32x2*>(static_cast<float*>(p.C) + (size_t)row * N + col) = f32x2{v[0], v[1]};
-          }
-        }
-      } else {
 #pragma unroll
-        for (int cb = 0; cb < WNC; ++cb) {
-          const int col = n0 + wn * WCOLS + 32 * cb + c;
-          if (col >= N) continue;
-          const float v = p.ep.any ? epilogue_value(p.ep, acc[rb][cb][i], row, col, N) : acc[rb][cb][i];
-          if (p.out_bf16)
-            static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(v);
-          else
-            static_cast<float*>(p.C)[(size_t)row * N + col] = v;
+          for (int cb = 0; cb < WNC; ++cb) {
+            const int col = n0 + wn * WCOLS + 32 * cb + c;
+            if (col >= N) continue;
+            const float v = kFused ? epilogue_value(p.ep, acc[rb][cb][i], row, col, N) : acc[rb][cb][i];
+            if (bf16)
+              static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(v);
+            else
+              static_cast<float*>(p.C)[(size_t)row * N + col] = v;
+          }
         }
       }
     }
-  }
+  };
+  if (p.ep.any)
+    store(StoreKind<true>{}, OutKind<2>{});
+  else if (p.out_bf16)
+    store(StoreKind<false>{}, OutKind<1>{});
+  else
+    store(StoreKind<false>{}, OutKind<0>{});
 }
 
 template <int LAYOUT, int WM, int WN, int RB, int WNC, int NS>

@@ -1,0 +1,438 @@
+// Hand-scheduled tiled MFMA kernel (M > 32, [K/2,N] weights, K % 64 == 0):
+// 128 x 256 x 64 tiles, 4 waves of 64 x 128, two CTAs per CU.  The production
+// kernel of the tiled family for the reference layout.
+//
+// Why it is built this way (measured on MI355X, dit_up 4096 x 12288 x 3072):
+//  * v_mfma_f32_16x16x32_bf16 sustains 1.68 PF/s (one wave per SIMD) and
+//    1.91 PF/s (two) on random bf16 operands, against 1.45 / 1.72 PF/s for
+//    v_mfma_f32_32x32x16_bf16: the 16x16x32 form is the faster one on data
+//    that toggles (both reach ~2.2-2.35 PF/s on constant operands).
+//  * Two waves per SIMD from two independent CTAs: one CTA's barrier, LDS
+//    latency and DMA issue overlap the other CTA's MFMAs (one 4-wave CTA per
+//    CU spent ~40 % of every stage in such bubbles).
+//  * The compiler's schedule issues LDS operand reads one or two MFMAs before
+//    their use.  Here every LDS read, convert, MFMA, LDS DMA, wait and
+//    barrier in the main loop is its own volatile asm statement, so their
+//    order is exactly the program order and the compiler only allocates
+//    registers; the waits are counted by hand (it cannot see the asm loads).
+//
+// Stage t (64 K) = sub-steps (t,0) and (t,1) of 32 K, 32 MFMAs each:
+//   (t,0): LDS reads of (t,1)'s raw B words and A operands; 32 MFMAs with one
+//          convert after each (see below); lgkmcnt waits.
+//   (t,1): s_waitcnt vmcnt (this wave's DMAs of stage t+1) + s_barrier, which
+//          publishes stage t+1 and retires stage t's ring slot (every read of
+//          stage t was issued and waited for in (t,0)); LDS reads of
+//          (t+1,0)'s operands and stage t+1's scales; the LDS DMAs of stage
+//          t+3 into the retired slot, spread over the MFMAs; 32 MFMAs with
+//          converts.
+//   Three ring slots hold stages t+1 (published), t+2 (in flight) and t+3
+//   (issued): a stage's loads get two stages of lead before their barrier.
+// Converts: MFMA block cb = 0..7 of a sub-step (4 MFMAs, one per 16-row
+// block) is followed by the four converts of B operand cb-2 of the NEXT
+// sub-step (its register's last reader was block cb-2); blocks 0, 1 convert
+// this sub-step's operands 6, 7.  Raw words are therefore read one sub-step
+// ahead into a double buffer, A operands likewise.
+//
+// Stage in LDS (24.25 KB):
+//   A  [128 rows][128 B]; 16-byte chunk c of row r at c ^ (r & 7) ^ ((r >> 3) & 1)
+//   B  [32 K-pair rows][256 B]; 16-byte chunk c of row R at c ^ 4 * ((R >> 2) & 3)
+//   S  [2 K groups][256 B] E8M0 scales of the stage's columns
+// MFMA v_mfma_f32_16x16x32_bf16: lane l holds A row l % 16, K 8(l / 16) .. +7
+// of the 32-K sub-step, and B column 4c + j of a 64-column group (c = l % 16,
+// MFMA j of the group): byte j of the four K-pair rows 4(l / 16) .. +3; the
+// result holds rows 4(l / 16) .. +3 of that column.
+//
+// Reference counterpart: the K loop of strategy_j / strategy_m
+// (csrc/strategy_j_synthesis.cu:120-170, csrc/strategy_m_asm.cu:131-185).
+#include "mxfp4_device.h"
+#include "mxfp4_kernels.h"
+
+namespace mxfp4 {
+namespace {
+
+constexpr int kBM = 128, kBN = 256, kBK = 64;
+constexpr int kWaves = 4;                       // 2 x 2 (M x N)
+constexpr int kThreads = kWaves * 64;
+constexpr int kRB = 4, kCB = 8;                 // 16-row x 16-column MFMA blocks per wave (64 x 128)
+constexpr int kABytes = kBM * kBK * 2;          // 16 KB
+constexpr int kBBytes = kBN * kBK / 2;          // 8 KB
+constexpr int kSBytes = 2 * kBN;                // 512 B
+constexpr int kStage = kABytes + kBBytes + kSBytes;
+constexpr int kNS = 3;                          // LDS ring depth
+constexpr int kLds = kNS * kStage + 256;        // + the window of the idle scale DMAs
+constexpr int kADma = kABytes / 1024 / kWaves;  // 4 per wave per stage
+constexpr int kBDma = kBBytes / 1024 / kWaves;  // 2
+constexpr int kVmPerStage = kADma + kBDma + 1;  // + one scale DMA
+static_assert(2 * kLds <= 160 * 1024, "two CTAs per CU");
+static_assert(2 * kVmPerStage < 64, "vmcnt range");
+
+__device__ __forceinline__ int a_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+// ---- one instruction each; volatile keeps them in program order ------------
+template <int OFF>
+__device__ __forceinline__ bf16x8 lds_b128(uint32_t addr) {
+  bf16x8 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+template <int O0, int O1>
+__device__ __forceinline__ u32x2 lds_2st64(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(v) : "v"(addr), "i"(O0), "i"(O1));
+  return v;
+}
+// Byte SEL of w (two E2M1 codes) -> two bf16 scaled by s (the E8M0 byte in
+// the fp32 exponent field).
+template <int SEL>
+__device__ __forceinline__ uint32_t cvt_fp4(uint32_t w, float s) {
+  uint32_t r;
+  if constexpr (SEL == 0)
+    asm volatile("v_cvt_scalef32_pk_bf16_fp4 %0, %1, %2" : "=v"(r) : "v"(w), "v"(s));
+  else if constexpr (SEL == 1)
+    asm volatile("v_cvt_scalef32_pk_bf16_fp4 %0, %1, %2 op_sel:[1,0,0]" : "=v"(r) : "v"(w), "v"(s));
+  else if constexpr (SEL == 2)
+    asm volatile("v_cvt_scalef32_pk_bf16_fp4 %0, %1, %2 op_sel:[0,1,0]" : "=v"(r) : "v"(w), "v"(s));
+  else
+    asm volatile("v_cvt_scalef32_pk_bf16_fp4 %0, %1, %2 op_sel:[1,1,0]" : "=v"(r) : "v"(w), "v"(s));
+  return r;
+}
+__device__ __forceinline__ void mfma16(f32x4& acc, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N));
+}
+// The same wait, redefining w and x: compiler-scheduled code that reads them
+// (asm LDS reads' results) cannot move above it.
+template <int N>
+__device__ __forceinline__ void lgkm_wait(u32x2& w, u32x2& x) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(w), "+v"(x) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N));
+}
+__device__ __forceinline__ void barrier_asm() { asm volatile("s_barrier"); }
+// 16 (4) bytes per lane, global (desc + voffset + soffset) -> LDS m0 + 16 (4) * lane.
+__device__ __forceinline__ void dma16s(const desc_t& d, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(d), "s"(soff), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4s(const desc_t& d, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(d), "s"(soff), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ float e8m0_byte(uint32_t w, int j) {
+  return __builtin_bit_cast(float, ((w >> (8 * j)) & 0xFFu) << 23);
+}
+
+__global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int c = lane & 15, q = lane >> 4;
+
+  const int total = p.tiles_m * p.tiles_n * p.splits;
+  const int logical = xcd_chunked_id((int)blockIdx.x, total);
+  const int tile = logical / p.splits;
+  const int split = logical - tile * p.splits;
+  const int group_size = p.group_m * p.tiles_n;
+  const int group = tile / group_size;
+  const int first_m = group * p.group_m;
+  const int gm_rows = min(p.tiles_m - first_m, p.group_m);
+  const int in_group = tile - group * group_size;
+  const int tm = first_m + in_group % gm_rows;
+  const int tn = in_group / gm_rows;
+  const int m0 = tm * kBM, n0 = tn * kBN;
+
+  const int M = p.M, N = p.N, K = p.K;
+  const int s_begin = split * p.steps_per_split;
+  const int T = min(p.ksteps, s_begin + p.steps_per_split) - s_begin;
+
+  // ---- loop-invariant DMA offsets (the K step goes in soffset) ---------------
+  const desc_t dA = make_desc(p.A + (size_t)m0 * K);
+  const desc_t dB = make_desc(p.B + n0);
+  const desc_t dS = make_desc(p.S + n0);
+  const desc_t dNull = make_desc(p.A, 0u);  // every lane out of range: writes zeros
+  uint32_t va[kADma];                       // A: DMA i covers rows 8i .. 8i+7
+#pragma unroll
+  for (int ii = 0; ii < kADma; ++ii) {
+    const int i = wave * kADma + ii;
+    const int row = i * 8 + (lane >> 3);
+    const int lc = (lane & 7) ^ a_swz(row);
+    va[ii] = m0 + row < M ? (uint32_t)(row * K * 2 + lc * 16) : kOobOffset;
+  }
+  uint32_t vb[kBDma];                       // B: DMA i covers K-pair rows 4i .. 4i+3
+#pragma unroll
+  for (int ii = 0; ii < kBDma; ++ii) {
+    const int qq = (wave * kBDma + ii) * 64 + lane;
+    const int row = qq >> 4;
+    const int lc = (qq & 15) ^ (4 * ((row >> 2) & 3));
+    vb[ii] = n0 + lc * 16 < N ? (uint32_t)(row * N + lc * 16) : kOobOffset;
+  }
+  // scales: waves 0, 1 move K group rows 0, 1 of the stage (256 columns each);
+  // waves 2, 3 issue the same DMA into a spare window so every wave counts
+  // the same number of loads per stage.
+  const bool sc_wave = wave < 2;
+  const uint32_t vs = sc_wave && n0 + 4 * lane < N ? (uint32_t)(wave * N + 4 * lane) : kOobOffset;
+  const uint32_t sc_lds = sc_wave ? (uint32_t)(kABytes + kBBytes + 256 * wave) : 0u;
+
+  auto issue_a = [&](int ii, int slot, int step, bool live) __attribute__((always_inline)) {
+    dma16s(live ? dA : dNull, lds0 + slot * kStage + (wave * kADma + ii) * 1024, va[ii],
+           (uint32_t)step * (kBK * 2));
+  };
+  auto issue_b = [&](int ii, int slot, int step, bool live) __attribute__((always_inline)) {
+    dma16s(live ? dB : dNull, lds0 + slot * kStage + kABytes + (wave * kBDma + ii) * 1024, vb[ii],
+           (uint32_t)step * (kBK / 2) * (uint32_t)N);
+  };
+  auto issue_s = [&](int slot, int step, bool live) __attribute__((always_inline)) {
+    dma4s(live ? dS : dNull, sc_wave ? lds0 + slot * kStage + sc_lds : lds0 + kNS * kStage, vs,
+          (uint32_t)step * 2u * (uint32_t)N);
+  };
+  // DMA number d (0 .. kVmPerStage-1) of a stage
+  auto issue_dma = [&](int d, int slot, int step, bool live) __attribute__((always_inline)) {
+    if (d < kADma)
+      issue_a(d, slot, step, live);
+    else if (d < kADma + kBDma)
+      issue_b(d - kADma, slot, step, live);
+    else
+      issue_s(slot, step, live);
+  };
+
+  // ---- loop-invariant LDS read offsets ---------------------------------------
+  uint32_t a_off[2];  // per sub-step; 16-row blocks are +2048 (immediate)
+  {
+    const int row = wm * 64 + c;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) a_off[sub] = (uint32_t)(row * 128 + (((sub * 4 + q) ^ a_swz(row)) * 16));
+  }
+  // B: K-pair row sub*16 + 4q + i, column byte wn*128 + 64g + 4c (group g);
+  // the row swizzle depends on q only.
+  uint32_t b_off[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int colb = wn * 128 + 64 * g + 4 * c;
+    b_off[g] = (uint32_t)(kABytes + 4 * q * kBN + (((colb >> 4) ^ (4 * q)) * 16) + (colb & 15));
+  }
+  const uint32_t s_off = (uint32_t)(kABytes + kBBytes + wn * 128 + 4 * c);  // + 64 g
+
+  f32x4 acc[kRB][kCB];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (T > 0) {
+    bf16x8 a[2][kRB];    // A operands, double-buffered by sub-step
+    uint32_t raw[2][8];  // raw B words (group g, row i at 4g + i), double-buffered
+    bf16x8 b[kCB];       // converted B operands, block cb = 4g + j
+    float sc[2][kCB];    // scales (K group of the sub-step) per block: current stage
+    float scn[2][kCB];   // the next stage's (read in (t,1))
+
+    auto read_raw = [&](uint32_t base, int sub, uint32_t (&r)[8]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const uint32_t addr = base + b_off[g];
+        u32x2 x, y;
+        if (sub == 0) {
+          x = lds_2st64<0, 1>(addr);
+          y = lds_2st64<2, 3>(addr);
+        } else {
+          x = lds_2st64<16, 17>(addr);
+          y = lds_2st64<18, 19>(addr);
+        }
+        r[4 * g + 0] = x.x; r[4 * g + 1] = x.y; r[4 * g + 2] = y.x; r[4 * g + 3] = y.y;
+      }
+    };
+    auto read_a = [&](uint32_t base, int sub, bf16x8 (&o)[kRB]) __attribute__((always_inline)) {
+      const uint32_t addr = base + a_off[sub];
+      o[0] = lds_b128<0>(addr);
+      o[1] = lds_b128<2048>(addr);
+      o[2] = lds_b128<4096>(addr);
+      o[3] = lds_b128<6144>(addr);
+    };
+    // scale words: w = (K group 0, 1) of column group 0, x = of column group 1
+    auto read_scales = [&](uint32_t base, u32x2& w, u32x2& x) __attribute__((always_inline)) {
+      w = lds_2st64<0, 1>(base + s_off);
+      x = lds_2st64<0, 1>(base + s_off + 64);
+    };
+    auto scales_from = [&](u32x2 w, u32x2 x, float (&s)[2][kCB]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s[kg][j] = e8m0_byte(kg ? w.y : w.x, j);
+          s[kg][4 + j] = e8m0_byte(kg ? x.y : x.x, j);
+        }
+    };
+    // the four converts of B operand cb (= 4g + j) from raw words r
+    auto convert = [&](int cb, const uint32_t (&r)[8], float s) __attribute__((always_inline)) {
+      const int g = cb >> 2, j = cb & 3;
+      const uint32_t* w = r + 4 * g;
+      u32x4 v;
+      switch (j) {
+        case 0: v = u32x4{cvt_fp4<0>(w[0], s), cvt_fp4<0>(w[1], s), cvt_fp4<0>(w[2], s), cvt_fp4<0>(w[3], s)}; break;
+        case 1: v = u32x4{cvt_fp4<1>(w[0], s), cvt_fp4<1>(w[1], s), cvt_fp4<1>(w[2], s), cvt_fp4<1>(w[3], s)}; break;
+        case 2: v = u32x4{cvt_fp4<2>(w[0], s), cvt_fp4<2>(w[1], s), cvt_fp4<2>(w[2], s), cvt_fp4<2>(w[3], s)}; break;
+        default: v = u32x4{cvt_fp4<3>(w[0], s), cvt_fp4<3>(w[1], s), cvt_fp4<3>(w[2], s), cvt_fp4<3>(w[3], s)}; break;
+      }
+      b[cb] = __builtin_bit_cast(bf16x8, v);
+    };
+
+    // ---- prologue: stages 0, 1, 2 in flight; operands of (0,0) ---------------
+#pragma unroll
+    for (int st = 0; st < kNS; ++st)
+#pragma unroll
+      for (int d = 0; d < kVmPerStage; ++d) issue_dma(d, st, s_begin + st, st < T);
+    vm_wait<(kNS - 1) * kVmPerStage>();
+    barrier_asm();
+    {
+      u32x2 w, x;
+      read_scales(lds0, w, x);
+      read_raw(lds0, 0, raw[0]);
+      read_a(lds0, 0, a[0]);
+      lgkm_wait<0>(w, x);
+      scales_from(w, x, sc);
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) convert(cb, raw[0], sc[0][cb]);
+    }
+
+    for (int t = 0; t < T; ++t) {
+      const uint32_t base = lds0 + (t % kNS) * kStage;
+      const uint32_t nbase = lds0 + ((t + 1) % kNS) * kStage;
+      const int dslot = t % kNS;  // slot retired by (t,1)'s barrier; stage t+3 goes there
+      const int dstep = s_begin + t + kNS;
+      const bool dlive = t + kNS < T;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const int pc = sub, pn = sub ^ 1;  // raw / A buffers of this and the next sub-step
+        u32x2 w = {0u, 0u}, x = {0u, 0u};
+        if (sub == 0) {
+          read_raw(base, 1, raw[pn]);
+          read_a(base, 1, a[pn]);
+        } else {
+          // publish stage t+1: this wave's DMAs for it are done (stage t+2's
+          // are the ones in flight)
+          vm_wait<kVmPerStage>();
+          barrier_asm();
+          read_scales(nbase, w, x);
+          read_raw(nbase, 0, raw[pn]);
+          read_a(nbase, 0, a[pn]);
+        }
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb) {
+#pragma unroll
+          for (int rb = 0; rb < kRB; ++rb) {
+            mfma16(acc[rb][cb], a[pc][rb], b[cb]);
+            // stage t+3's DMAs, one after every fourth MFMA from block 2 on
+            if (sub == 1 && rb == 3 && cb >= 1 && cb - 1 < kVmPerStage) issue_dma(cb - 1, dslot, dstep, dlive);
+          }
+          if (cb == 1) {
+            // the next sub-step's raw words (and stage t+1's scales) landed
+            if (sub == 0) {
+              lgkm_wait<kRB>();
+            } else {
+              lgkm_wait<kRB>(w, x);
+              scales_from(w, x, scn);
+            }
+          }
+          // converts: blocks 0, 1 finish this sub-step's operands 6, 7; blocks
+          // 2 .. 7 convert the next sub-step's operands 0 .. 5
+          if (cb < 2)
+            convert(cb + 6, raw[pc], sc[sub][cb + 6]);
+          else
+            convert(cb - 2, raw[pn], sub == 0 ? sc[1][cb - 2] : scn[0][cb - 2]);
+        }
+        lgkm_wait<0>();
+        if (sub == 1) {
+#pragma unroll
+          for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+            for (int cb = 0; cb < kCB; ++cb) sc[kg][cb] = scn[kg][cb];
+        }
+      }
+    }
+    // the DMAs of the stages past the end still write the ring; the MFMAs
+    // must finish before the accumulators are read
+    vm_wait<0>();
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7");
+    __syncthreads();
+  }
+
+  // ---- split-K fix-up (the pipelined kernel's protocol) ------------------------
+  int* s_last = reinterpret_cast<int*>(smem);
+  if (p.splits > 1) {
+    constexpr int Q = kRB * kCB;  // f32x4 per thread
+    constexpr uint32_t SLOT = (uint32_t)Q * kThreads * 16;
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(reinterpret_cast<uint8_t*>(p.partials) + (size_t)tile * p.splits * SLOT);
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb)
+        store_coherent(rp, split * SLOT + (uint32_t)((rb * kCB + cb) * kThreads + threadIdx.x) * 16, acc[rb][cb]);
+    if (!splitk_arrive_last(p.counters + tile, (uint32_t)p.splits, s_last)) return;
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+        const uint32_t off = (uint32_t)((rb * kCB + cb) * kThreads + threadIdx.x) * 16;
+        f32x4 sum = load_coherent4(rp, off);
+        for (int sp = 1; sp < p.splits; ++sp) sum += load_coherent4(rp, sp * SLOT + off);
+        acc[rb][cb] = sum;
+      }
+  }
+
+  // ---- epilogue: 4 adjacent columns (blocks 4g .. 4g+3) per lane and row --------
+  // Plain and fused stores are separate loops, chosen once (see StoreKind).
+  auto store = [&](auto fused, auto out) __attribute__((always_inline)) {
+    constexpr bool kFused = decltype(fused)::value;
+    const bool bf16 = decltype(out)::value == 2 ? p.out_bf16 != 0 : decltype(out)::value == 1;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int col = n0 + wn * 128 + 64 * g + 4 * c;
+      if (col >= N) continue;
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = m0 + wm * 64 + rb * 16 + 4 * q + i;
+          if (row >= M) continue;
+          float v[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            v[j] = kFused ? epilogue_value(p.ep, acc[rb][4 * g + j][i], row, col + j, N) : acc[rb][4 * g + j][i];
+          if (bf16) {
+            const u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = w;
+          } else {
+            *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col) = f32x4{v[0], v[1], v[2], v[3]};
+          }
+        }
+      }
+    }
+  };
+  if (p.ep.any)
+    store(StoreKind<true>{}, OutKind<2>{});
+  else if (p.out_bf16)
+    store(StoreKind<false>{}, OutKind<1>{});
+  else
+    store(StoreKind<false>{}, OutKind<0>{});
+}
+
+}  // namespace
+
+bool tiled_sched_available(int layout, const TiledShape& s) {
+  return layout == kLayoutKN && s.bm() == kBM && s.bn() == kBN && s.wm * s.wn == kWaves && s.stages == kNS;
+}
+
+hipError_t launch_tiled_sched(int layout, const TiledShape& shape, const TiledArgs& args, hipStream_t stream) {
+  if (!tiled_sched_available(layout, shape) || args.K % kBK != 0) return hipErrorInvalidValue;
+  const int grid = args.tiles_m * args.tiles_n * args.splits;
+  hipLaunchKernelGGL(tiled_sched_kn_kernel, dim3(grid), dim3(kThreads), 0, stream, args);
+  return hipGetLastError();
+}
+
+}  // namespace mxfp4

@@ -121,8 +121,9 @@ def test_generic_kernel_odd_n(kk):
         assert mo.strict_violations(out, ref, K) == 0
 
 
-TILED_VARIANTS = range(15)
+TILED_VARIANTS = range(16)
 PIPE_VARIANTS = range(6, 15)  # pipelined kernel; [N,K/2] needs K % 128 == 0
+SCHED_VARIANT = 15            # hand-scheduled kernel: [K/2,N] and K % 64 == 0 only
 GEMV_VARIANTS = range(15)
 
 
@@ -137,13 +138,40 @@ def test_every_tiled_variant_and_split(kk, layout, K):
         for split in (1, 2, 3, (K + 63) // 64):  # the last: one 64-K step per split
             log(f"case tiled variant={v} split={split} layout={layout} K={K}")
             plan = (kk.KERNEL_TILED, v, split)
-            if layout == "nk" and K % 128 and v in PIPE_VARIANTS:
+            if (layout == "nk" and K % 128 and v in PIPE_VARIANTS) or (
+                    v == SCHED_VARIANT and (layout != "kn" or K % 64)):
                 with pytest.raises(RuntimeError, match="invalid argument"):
                     run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=plan)
                 continue
             out = run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=plan)
             bad = mo.strict_violations(out, ref, K)
             assert bad == 0, f"variant {v} split {split}: {bad} bad"
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 528, 640), (64, 256, 64), (513, 1040, 1536)])
+def test_sched_kernel_tails_and_splits(kk, M, N, K):
+    """Hand-scheduled kernel: M / N tails (N % 256 != 0), splits down to one
+    64-K step, fp32 and bf16 out, against the float64 oracle; every split
+    count sums the same 64-K partial products (fp32), so splits agree to
+    within fp32 reassociation, and bf16 out is the fp32 result rounded."""
+    import torch
+
+    A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=33)
+    ref = oracle_f64(A_bits, W, S)
+    plan = lambda split: (kk.KERNEL_TILED, SCHED_VARIANT, split)
+    base = None
+    for split in sorted({s for s in (1, 2, 3, K // 64) if s <= K // 64}):
+        log(f"case sched M={M} N={N} K={K} split={split}")
+        out = run_gemm(kk, A_bits, W, S, "kn", torch.float32, plan=plan(split))
+        assert mo.strict_violations(out, ref, K) == 0, f"split {split}"
+        again = run_gemm(kk, A_bits, W, S, "kn", torch.float32, plan=plan(split))
+        assert np.array_equal(out, again), f"split {split}: not deterministic"
+        out16 = run_gemm(kk, A_bits, W, S, "kn", torch.bfloat16, plan=plan(split))
+        assert np.array_equal(out16, mo.bf16_bits_to_f32(mo.f32_to_bf16_bits(out))), f"split {split}: bf16 rounding"
+        if base is None:
+            base = out
+        else:
+            np.testing.assert_allclose(out, base, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
 
 
 @pytest.mark.parametrize("layout", ["kn", "nk"])
