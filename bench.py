@@ -253,7 +253,9 @@ def main():
                           "traffic": profile_traffic("gemv_decode_m16_kn")},
         }
 
-    result["roofline"]["traffic"] = profile_traffic(f"tiled_dit_up_{args.layout}")
+    # the committed rocprof summary of the kernel the plan runs
+    family = "tiled_sched" if up["plan"].startswith("tiled-sched") else "tiled"
+    result["roofline"]["traffic"] = profile_traffic(f"{family}_dit_up_{args.layout}")
     if args.calibrate_copy:
         copy_calibration()
     if not args.no_cpu:

@@ -44,6 +44,8 @@
 //
 // Reference counterpart: the K loop of strategy_j / strategy_m
 // (csrc/strategy_j_synthesis.cu:120-170, csrc/strategy_m_asm.cu:131-185).
+#include <type_traits>
+
 #include "mxfp4_device.h"
 #include "mxfp4_kernels.h"
 
@@ -115,11 +117,18 @@ __device__ __forceinline__ void vm_wait() {
 }
 __device__ __forceinline__ void barrier_asm() { asm volatile("s_barrier"); }
 // 16 (4) bytes per lane, global (desc + voffset + soffset) -> LDS m0 + 16 (4) * lane.
+// soff is wave-uniform; readfirstlane keeps it in an SGPR when the compiler
+// cannot prove that.  The compiler may then write that SGPR with a VALU
+// instruction (v_readfirstlane) right before the asm, and its hazard checks
+// do not look inside inline asm: a VMEM instruction reading an SGPR that a
+// VALU instruction wrote needs 5 wait states, hence the s_nop.
 __device__ __forceinline__ void dma16s(const desc_t& d, uint32_t lds, uint32_t voff, uint32_t soff) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(d), "s"(soff), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(d),
+               "s"(__builtin_amdgcn_readfirstlane(soff)), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4s(const desc_t& d, uint32_t lds, uint32_t voff, uint32_t soff) {
-  asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(d), "s"(soff), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(d),
+               "s"(__builtin_amdgcn_readfirstlane(soff)), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ float e8m0_byte(uint32_t w, int j) {
   return __builtin_bit_cast(float, ((w >> (8 * j)) & 0xFFu) << 23);
@@ -206,7 +215,7 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
   {
     const int row = wm * 64 + c;
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) a_off[sub] = (uint32_t)(row * 128 + (((sub * 4 + q) ^ a_swz(row)) * 16));
+    for (int sub = 0; sub < 2; ++sub) a_off[sub] = lds0 + (uint32_t)(row * 128 + (((sub * 4 + q) ^ a_swz(row)) * 16));
   }
   // B: K-pair row sub*16 + 4q + i, column byte wn*128 + 64g + 4c (group g);
   // the row swizzle depends on q only.
@@ -214,9 +223,9 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
     const int colb = wn * 128 + 64 * g + 4 * c;
-    b_off[g] = (uint32_t)(kABytes + 4 * q * kBN + (((colb >> 4) ^ (4 * q)) * 16) + (colb & 15));
+    b_off[g] = lds0 + (uint32_t)(kABytes + 4 * q * kBN + (((colb >> 4) ^ (4 * q)) * 16) + (colb & 15));
   }
-  const uint32_t s_off = (uint32_t)(kABytes + kBBytes + wn * 128 + 4 * c);  // + 64 g
+  const uint32_t s_off = lds0 + (uint32_t)(kABytes + kBBytes + wn * 128 + 4 * c);  // + 64 g
 
   f32x4 acc[kRB][kCB];
 #pragma unroll
@@ -228,43 +237,46 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
     bf16x8 a[2][kRB];    // A operands, double-buffered by sub-step
     uint32_t raw[2][8];  // raw B words (group g, row i at 4g + i), double-buffered
     bf16x8 b[kCB];       // converted B operands, block cb = 4g + j
-    float sc[2][kCB];    // scales (K group of the sub-step) per block: current stage
-    float scn[2][kCB];   // the next stage's (read in (t,1))
+    float sc[2][kCB];    // scales per K group of the stage and block
 
-    auto read_raw = [&](uint32_t base, int sub, uint32_t (&r)[8]) __attribute__((always_inline)) {
+    // LDS reads of ring slot SL (a compile-time constant: every address is a
+    // loop-invariant register plus an immediate offset; kStage = 98 x 256 B).
+    auto read_raw = [&](auto slot_c, int sub, uint32_t (&r)[8]) __attribute__((always_inline)) {
+      constexpr int O = decltype(slot_c)::value * (kStage / 256);
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
-        const uint32_t addr = base + b_off[g];
         u32x2 x, y;
         if (sub == 0) {
-          x = lds_2st64<0, 1>(addr);
-          y = lds_2st64<2, 3>(addr);
+          x = lds_2st64<O + 0, O + 1>(b_off[g]);
+          y = lds_2st64<O + 2, O + 3>(b_off[g]);
         } else {
-          x = lds_2st64<16, 17>(addr);
-          y = lds_2st64<18, 19>(addr);
+          x = lds_2st64<O + 16, O + 17>(b_off[g]);
+          y = lds_2st64<O + 18, O + 19>(b_off[g]);
         }
         r[4 * g + 0] = x.x; r[4 * g + 1] = x.y; r[4 * g + 2] = y.x; r[4 * g + 3] = y.y;
       }
     };
-    auto read_a = [&](uint32_t base, int sub, bf16x8 (&o)[kRB]) __attribute__((always_inline)) {
-      const uint32_t addr = base + a_off[sub];
-      o[0] = lds_b128<0>(addr);
-      o[1] = lds_b128<2048>(addr);
-      o[2] = lds_b128<4096>(addr);
-      o[3] = lds_b128<6144>(addr);
+    auto read_a = [&](auto slot_c, int sub, bf16x8 (&o)[kRB]) __attribute__((always_inline)) {
+      constexpr int O = decltype(slot_c)::value * kStage;
+      const uint32_t addr = a_off[sub];
+      o[0] = lds_b128<O + 0>(addr);
+      o[1] = lds_b128<O + 2048>(addr);
+      o[2] = lds_b128<O + 4096>(addr);
+      o[3] = lds_b128<O + 6144>(addr);
     };
     // scale words: w = (K group 0, 1) of column group 0, x = of column group 1
-    auto read_scales = [&](uint32_t base, u32x2& w, u32x2& x) __attribute__((always_inline)) {
-      w = lds_2st64<0, 1>(base + s_off);
-      x = lds_2st64<0, 1>(base + s_off + 64);
+    auto read_scales = [&](auto slot_c, u32x2& w, u32x2& x) __attribute__((always_inline)) {
+      constexpr int O = decltype(slot_c)::value * (kStage / 256);
+      w = lds_2st64<O, O + 1>(s_off);
+      x = lds_2st64<O, O + 1>(s_off + 64);
     };
-    auto scales_from = [&](u32x2 w, u32x2 x, float (&s)[2][kCB]) __attribute__((always_inline)) {
+    auto scales_from = [&](u32x2 w, u32x2 x) __attribute__((always_inline)) {
 #pragma unroll
       for (int kg = 0; kg < 2; ++kg)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          s[kg][j] = e8m0_byte(kg ? w.y : w.x, j);
-          s[kg][4 + j] = e8m0_byte(kg ? x.y : x.x, j);
+          sc[kg][j] = e8m0_byte(kg ? w.y : w.x, j);
+          sc[kg][4 + j] = e8m0_byte(kg ? x.y : x.x, j);
         }
     };
     // the four converts of B operand cb (= 4g + j) from raw words r
@@ -290,70 +302,75 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
     barrier_asm();
     {
       u32x2 w, x;
-      read_scales(lds0, w, x);
-      read_raw(lds0, 0, raw[0]);
-      read_a(lds0, 0, a[0]);
+      read_scales(std::integral_constant<int, 0>{}, w, x);
+      read_raw(std::integral_constant<int, 0>{}, 0, raw[0]);
+      read_a(std::integral_constant<int, 0>{}, 0, a[0]);
       lgkm_wait<0>(w, x);
-      scales_from(w, x, sc);
+      scales_from(w, x);
 #pragma unroll
       for (int cb = 0; cb < kCB; ++cb) convert(cb, raw[0], sc[0][cb]);
     }
 
-    for (int t = 0; t < T; ++t) {
-      const uint32_t base = lds0 + (t % kNS) * kStage;
-      const uint32_t nbase = lds0 + ((t + 1) % kNS) * kStage;
-      const int dslot = t % kNS;  // slot retired by (t,1)'s barrier; stage t+3 goes there
-      const int dstep = s_begin + t + kNS;
+    // Stage t in ring slot SL = t % kNS (the caller unrolls the slots).
+    auto stage = [&](auto slot_c, int t) __attribute__((always_inline)) {
+      constexpr int SL = decltype(slot_c)::value;
+      using Next = std::integral_constant<int, (SL + 1) % kNS>;
+      const int dstep = s_begin + t + kNS;  // stage t+3 goes into slot SL, retired by (t,1)'s barrier
       const bool dlive = t + kNS < T;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         const int pc = sub, pn = sub ^ 1;  // raw / A buffers of this and the next sub-step
         u32x2 w = {0u, 0u}, x = {0u, 0u};
         if (sub == 0) {
-          read_raw(base, 1, raw[pn]);
-          read_a(base, 1, a[pn]);
+          read_raw(slot_c, 1, raw[pn]);
+          read_a(slot_c, 1, a[pn]);
         } else {
           // publish stage t+1: this wave's DMAs for it are done (stage t+2's
           // are the ones in flight)
           vm_wait<kVmPerStage>();
           barrier_asm();
-          read_scales(nbase, w, x);
-          read_raw(nbase, 0, raw[pn]);
-          read_a(nbase, 0, a[pn]);
+          read_scales(Next{}, w, x);
+          read_raw(Next{}, 0, raw[pn]);
+          read_a(Next{}, 0, a[pn]);
         }
 #pragma unroll
         for (int cb = 0; cb < kCB; ++cb) {
 #pragma unroll
           for (int rb = 0; rb < kRB; ++rb) {
             mfma16(acc[rb][cb], a[pc][rb], b[cb]);
-            // stage t+3's DMAs, one after every fourth MFMA from block 2 on
-            if (sub == 1 && rb == 3 && cb >= 1 && cb - 1 < kVmPerStage) issue_dma(cb - 1, dslot, dstep, dlive);
+            // stage t+3's DMAs, one after every fourth MFMA from block 1 on
+            if (sub == 1 && rb == 3 && cb >= 1 && cb - 1 < kVmPerStage) issue_dma(cb - 1, SL, dstep, dlive);
           }
+          // converts: blocks 0, 1 finish this sub-step's operands 6, 7 (K
+          // group `sub`); blocks 2 .. 7 convert the next sub-step's operands
+          // 0 .. 5 (K group 1 of this stage, or 0 of the next)
           if (cb == 1) {
             // the next sub-step's raw words (and stage t+1's scales) landed
             if (sub == 0) {
               lgkm_wait<kRB>();
+              convert(7, raw[pc], sc[0][7]);
             } else {
               lgkm_wait<kRB>(w, x);
-              scales_from(w, x, scn);
+              convert(7, raw[pc], sc[1][7]);
+              scales_from(w, x);  // stage t's scales are dead from here
             }
+          } else if (cb == 0) {
+            convert(6, raw[pc], sc[sub][6]);
+          } else {
+            convert(cb - 2, raw[pn], sc[sub == 0 ? 1 : 0][cb - 2]);
           }
-          // converts: blocks 0, 1 finish this sub-step's operands 6, 7; blocks
-          // 2 .. 7 convert the next sub-step's operands 0 .. 5
-          if (cb < 2)
-            convert(cb + 6, raw[pc], sc[sub][cb + 6]);
-          else
-            convert(cb - 2, raw[pn], sub == 0 ? sc[1][cb - 2] : scn[0][cb - 2]);
         }
         lgkm_wait<0>();
-        if (sub == 1) {
-#pragma unroll
-          for (int kg = 0; kg < 2; ++kg)
-#pragma unroll
-            for (int cb = 0; cb < kCB; ++cb) sc[kg][cb] = scn[kg][cb];
-        }
       }
+    };
+    for (int t = 0; t < T; t += kNS) {
+      stage(std::integral_constant<int, 0>{}, t);
+      if (t + 1 >= T) break;
+      stage(std::integral_constant<int, 1>{}, t + 1);
+      if (t + 2 >= T) break;
+      stage(std::integral_constant<int, 2>{}, t + 2);
     }
+    static_assert(kNS == 3, "the stage loop unrolls three ring slots");
     // the DMAs of the stages past the end still write the ring; the MFMAs
     // must finish before the accumulators are read
     vm_wait<0>();
