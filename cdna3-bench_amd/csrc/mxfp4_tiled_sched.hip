@@ -421,11 +421,14 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             v[j] = kFused ? epilogue_value(p.ep, acc[rb][4 * g + j][i], row, col + j, N) : acc[rb][4 * g + j][i];
+          // C is not read again here: non-temporal stores (measured ~2 %
+          // faster on dit_up, whose rounds end in a synchronized store burst)
           if (bf16) {
             const u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col) = w;
+            __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + (size_t)row * N + col));
           } else {
-            *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col) = f32x4{v[0], v[1], v[2], v[3]};
+            __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]},
+                                        reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)row * N + col));
           }
         }
       }
