@@ -78,7 +78,7 @@ def check(kk, M, N, K, layout, plan, seed=0):
 
 @pytest.mark.parametrize("layout,plan", [
     ("kn", (2, 6, 1)), ("kn", (2, 6, 3)), ("nk", (2, 10, 2)), ("g", (2, 6, 1)), ("p", (2, 10, 3)),
-    ("kn", (2, 1, 1)), ("nk", (2, 0, 2)),
+    ("kn", (2, 1, 1)), ("nk", (2, 0, 2)), ("kn", (2, 15, 1)), ("kn", (2, 15, 3)),
 ])
 def test_epilogue_tiled(kk, layout, plan):
     check(kk, 300, 512, 640, layout, plan)
@@ -117,12 +117,13 @@ def test_epilogue_k0_and_residual_is_c(kk):
     A_bits, W, Sc = mo.make_inputs(64, 256, 256, 120, 128, seed=4)
     Bk, Sk = mo.nk_to_kn(W, Sc)
     Ad, Bd, Sd = to_dev_bf16(A_bits), to_dev_u8(Bk), to_dev_u8(Sk)
-    log("case epilogue residual aliases C")
-    plain = kk.gemm(Ad, Bd, Sd, None, "kn", torch.float32)
-    C = torch.randn(64, 256, device="cuda")
-    old = C.clone()
-    kk.gemm(Ad, Bd, Sd, C, "kn", None, None, None, None, C)
-    assert torch.allclose(C, plain + old, rtol=1e-6, atol=1e-6)
+    for plan in (None, (kk.KERNEL_TILED, 15, 1)):  # auto, and the scheduled kernel's non-temporal stores
+        log(f"case epilogue residual aliases C plan={plan}")
+        plain = kk.gemm(Ad, Bd, Sd, None, "kn", torch.float32, plan)
+        C = torch.randn(64, 256, device="cuda")
+        old = C.clone()
+        kk.gemm(Ad, Bd, Sd, C, "kn", None, plan, None, None, C)
+        assert torch.allclose(C, plain + old, rtol=1e-6, atol=1e-6)
 
 
 def test_epilogue_argument_errors(kk):
