@@ -134,6 +134,11 @@ __device__ __forceinline__ float e8m0_byte(uint32_t w, int j) {
   return __builtin_bit_cast(float, ((w >> (8 * j)) & 0xFFu) << 23);
 }
 
+// kOut: 0 plain fp32 C, 1 plain bf16 C, 2 fused epilogue (either C type).  One
+// instantiation per store kind: with all three store loops in one kernel the
+// register allocator spills accumulators before the branch, so even the plain
+// stores went through scratch.
+template <int kOut>
 __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
@@ -434,12 +439,7 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
       }
     }
   };
-  if (p.ep.any)
-    store(StoreKind<true>{}, OutKind<2>{});
-  else if (p.out_bf16)
-    store(StoreKind<false>{}, OutKind<1>{});
-  else
-    store(StoreKind<false>{}, OutKind<0>{});
+  store(StoreKind<kOut == 2>{}, OutKind<kOut>{});
 }
 
 }  // namespace
@@ -451,7 +451,12 @@ bool tiled_sched_available(int layout, const TiledShape& s) {
 hipError_t launch_tiled_sched(int layout, const TiledShape& shape, const TiledArgs& args, hipStream_t stream) {
   if (!tiled_sched_available(layout, shape) || args.K % kBK != 0) return hipErrorInvalidValue;
   const int grid = args.tiles_m * args.tiles_n * args.splits;
-  hipLaunchKernelGGL(tiled_sched_kn_kernel, dim3(grid), dim3(kThreads), 0, stream, args);
+  if (args.ep.any)
+    hipLaunchKernelGGL(tiled_sched_kn_kernel<2>, dim3(grid), dim3(kThreads), 0, stream, args);
+  else if (args.out_bf16)
+    hipLaunchKernelGGL(tiled_sched_kn_kernel<1>, dim3(grid), dim3(kThreads), 0, stream, args);
+  else
+    hipLaunchKernelGGL(tiled_sched_kn_kernel<0>, dim3(grid), dim3(kThreads), 0, stream, args);
   return hipGetLastError();
 }
 
