@@ -81,6 +81,8 @@ const StreamShape kStream[] = {
     {2, 4, 2, 8, 8, 256},  // 2: M <= 32, split 1024 K (K <= 8192)
     {1, 8, 2, 2, 2, 512},  // 3: M <= 16, split 4096 K (K <= 8192)
     {2, 4, 2, 4, 4, 512},  // 4: M <= 32, split 2048 K (K <= 8192)
+    {1, 16, 2, 1, 1, 512}, // 5: whole K, M <= 16, K <= 8192 (K / 512 waves)
+    {1, 16, 2, 1, 1, 256}, // 6: whole K, M <= 16, K <= 4096 (K / 256 waves)
 };
 constexpr int kNumStream = sizeof(kStream) / sizeof(kStream[0]);
 constexpr int kStreamSpin = 4096;  // late-unit polls before counter arbitration
@@ -131,9 +133,16 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
   // K = 8192: 512-K waves with 2 splits beat 256-K waves with 4; both beat
   // this family by 1.3-1.7x).
   if (layout == kLayoutNK || layout == kLayoutP) {
-    static const int kPrefer16[] = {3, 0, 1}, kPrefer32[] = {4, 2};
-    const int* pref = two ? kPrefer32 : kPrefer16;
-    const int npref = two ? 2 : 3;
+    // M <= 8: the whole-K kernel first (256-K waves up to K = 4096).  It
+    // reads 32 x K activation bytes per CU, which at M = 16 is twice the CU's
+    // weight bytes; there the split-K kernel, which reuses each CTA's K range
+    // of activations across two column groups, is faster (measured at
+    // N = 8192 / 28672, K = 8192: whole-K 10.6 / 32.3 us at M = 1, 12.4 /
+    // 40.7 us at M = 8, 15.8 / 52.7 us at M = 16; split-K 12.7 / 41.5 us at
+    // M = 1, 13.1 / 42.7 us at M = 16).
+    static const int kPrefer8[] = {6, 5, 3, 0, 1}, kPrefer16[] = {3, 0, 1}, kPrefer32[] = {4, 2};
+    const int* pref = two ? kPrefer32 : M <= 8 ? kPrefer8 : kPrefer16;
+    const int npref = two ? 2 : M <= 8 ? 5 : 3;
     for (int i = 0; i < npref; ++i) {
       const StreamShape& st = kStream[pref[i]];
       if (stream_plan_ok(layout, M, N, K, st) && stream_ctas(st, N, K) >= 192) {
@@ -455,8 +464,11 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
     case MXFP4_KERNEL_STREAM: {
       if (plan->variant < 0 || plan->variant >= kNumStream) return hipErrorInvalidValue;
       const StreamShape& s = kStream[plan->variant];
-      snprintf(buf, buf_len, "stream mt%d w%d kw%d kr%d split%d", s.mt, s.waves, s.kw, s.k_split(),
-               plan->split_k);
+      if (s.nslot == 1 && s.smax == 1)
+        snprintf(buf, buf_len, "stream-whole mt%d kw%d split%d", s.mt, s.kw, plan->split_k);
+      else
+        snprintf(buf, buf_len, "stream mt%d w%d kw%d kr%d split%d", s.mt, s.waves, s.kw, s.k_split(),
+                 plan->split_k);
       return hipSuccess;
     }
     case MXFP4_KERNEL_TILED: {

@@ -531,6 +531,246 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
   }
 }
 
+// ---- whole-K streaming kernel (M <= 16, K <= 16 * KW) ----------------------
+// One CTA per 32-column group and K / KW waves, each owning K range
+// w*KW .. w*KW+KW-1 of the group: its weights (32 columns x KW/2 bytes) and
+// scales land in its own LDS slot, its activations (16 rows x KW) in VGPRs.
+// Every load of the CTA is issued at entry -- no split-K, no ring reuse, no
+// cross-CTA protocol -- so the only serial steps after the last byte lands
+// are the wave's remaining MFMAs, one barrier and an LDS reduction of the
+// waves' partial tiles (in wave order: bit-reproducible).
+//
+// All VMEM instructions here are asm, counted by hand: the activation loads
+// first (4 per 128 K), then the scale DMAs, then the weight DMAs.  A wait
+// that publishes loaded registers redefines them (asm "+v"), so no use can
+// be scheduled above it.
+template <int KW>
+struct WholeCfg {
+  static_assert(KW == 256 || KW == 512, "K per wave");
+  static constexpr int MAXW = 16;             // waves per CTA at most
+  static constexpr int STEPS = KW / 128;      // 4-MFMA steps per column block
+  static constexpr int CH = KW / 32;          // 16-byte chunks (and scale bytes) per column
+  static constexpr int CPD = 2048 / KW;       // columns per weight DMA ([N,K/2])
+  static constexpr int NI = 16 / CPD;         // weight DMAs per 16-column block
+  static constexpr int SLOT = 32 * KW / 2;    // weight bytes per wave
+  static constexpr int W_LOADS = SLOT / 1024;
+  static constexpr int SC_W = 32 * CH;        // scale bytes per wave
+  static constexpr int SC_LOADS = SC_W / 256;
+  static constexpr int A_LOADS = 4 * STEPS;
+  static constexpr int VM = A_LOADS + SC_LOADS + W_LOADS;
+  static constexpr int LDS = MAXW * (SLOT + SC_W);
+  static_assert(VM < 64, "vmcnt range");
+  static_assert(SLOT >= 16 * 32 * 4, "a wave's slot holds its 16 x 32 partial tile");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+__device__ __forceinline__ u32x4 asm_load16(const desc_t& d, uint32_t voff) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(d) : "memory");
+  return v;
+}
+// s_waitcnt vmcnt(N) that redefines the STEPS x 4 activation registers.
+template <int N, int STEPS>
+__device__ __forceinline__ void vm_wait_tie(u32x4 (&a)[STEPS][4]) {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+#pragma unroll
+  for (int t = 0; t < STEPS; ++t)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) asm volatile("" : "+v"(a[t][s]));
+}
+
+template <int LAYOUT, int KW>
+__global__ void __launch_bounds__(1024, 1) stream_whole_kernel(StreamArgs p) {
+  static_assert(LAYOUT == kLayoutNK || LAYOUT == kLayoutP, "weight layout");
+  using Cfg = WholeCfg<KW>;
+  constexpr int STEPS = Cfg::STEPS, CH = Cfg::CH, CPD = Cfg::CPD, NI = Cfg::NI, SLOT = Cfg::SLOT;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::LDS];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = (int)blockDim.x >> 6;  // K / KW
+  const int g = blockIdx.x;             // column group
+  const int M = p.M, N = p.N, K = p.K;
+  const int Kh = K >> 1, G = K >> 5;
+  const int c = lane & 15, q = lane >> 4;
+  const int kw0 = wave * KW;
+  uint8_t* const ws = smem + wave * SLOT;
+  uint8_t* const ss = smem + Cfg::MAXW * SLOT + wave * Cfg::SC_W;
+
+  // Issue order: the first half of the weights, the scales, the activations,
+  // the second half.  The weights' HBM requests go out first; the activation
+  // loads (L2 hits, 16 rows x KW x 2 bytes per wave -- twice the wave's
+  // weight bytes at M = 16) are taken in while those stream, and the first
+  // half's compute waits only for them.
+  // activations: lane (c, q) holds row c, K kw0 + 128t + 32q + 8s .. +7 in a[t][s]
+  u32x4 a[STEPS][4];
+  auto issue_a = [&]() __attribute__((always_inline)) {
+    const desc_t d = make_desc(p.A);
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        a[t][s] = asm_load16(d, c < M ? (uint32_t)((c * K + kw0 + 128 * t + 32 * q + 8 * s) * 2) : kOobOffset);
+  };
+  if constexpr (LAYOUT == kLayoutP) {
+    // scales: KW/64 blocks of 64 bytes; weights: KW/64 blocks of 1 KB, both
+    // contiguous in the panel
+    const desc_t d = make_desc(p.B + ((size_t)g * (K / kPK) + (kw0 >> 6)) * 1024);
+#pragma unroll
+    for (int i = 0; i < Cfg::W_LOADS / 2; ++i) dma16(d, ws + i * 1024, (uint32_t)(i * 1024 + 16 * lane));
+    const desc_t ds = make_desc(p.S + (size_t)g * (K / kPK) * 64 + kw0);
+#pragma unroll
+    for (int k = 0; k < Cfg::SC_LOADS; ++k) dma4(ds, ss + 256 * k, (uint32_t)(256 * k + 4 * lane));
+    issue_a();
+#pragma unroll
+    for (int i = Cfg::W_LOADS / 2; i < Cfg::W_LOADS; ++i) dma16(d, ws + i * 1024, (uint32_t)(i * 1024 + 16 * lane));
+  } else {
+    // weights: DMA i of block cb moves CPD whole column segments (KW/2
+    // bytes); chunk j of column 16cb + CPD*i + rr lands at 16-byte position
+    // (j + rot(i, rr)) % CH of its row (16 distinct bank slots per read)
+    const desc_t d = make_desc(p.B + (size_t)g * 32 * Kh);
+    const int rr = lane / CH;
+    auto issue_w = [&](int cb) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int col = 16 * cb + CPD * i + rr;
+        const int j = ((lane % CH) - chunk_rot<KW>(i, rr)) & (CH - 1);
+        const bool ok = g * 32 + col < N;
+        dma16(d, ws + (NI * cb + i) * 1024, ok ? (uint32_t)(col * Kh + (kw0 >> 1) + 16 * j) : kOobOffset);
+      }
+    };
+    issue_w(0);
+    // scales: [32 columns][CH bytes] of this wave's K range
+    {
+      const desc_t ds = make_desc(p.S + (size_t)g * 32 * G);
+#pragma unroll
+      for (int k = 0; k < Cfg::SC_LOADS; ++k) {
+        const int byte = 256 * k + 4 * lane;
+        const int col = byte / CH, b = byte % CH;
+        const bool ok = g * 32 + col < N;
+        dma4(ds, ss + 256 * k, ok ? (uint32_t)(col * G + kw0 / 32 + b) : kOobOffset);
+      }
+    }
+    issue_a();
+    issue_w(1);
+  }
+
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  if constexpr (LAYOUT == kLayoutP) {
+    // step t needs blocks 2t, 2t + 1 (chunk 4t + q = block 2t + q/2, lane
+    // slot 32 (q % 2) + column); its scale sits at the same slot of the
+    // block's 64 scale bytes
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t) {
+      // blocks 0 .. 2t+1 landed: at most min(W/2, W - 2t - 2) loads
+      // outstanding (the second half of the weights follows the activations)
+      constexpr int W = Cfg::W_LOADS;
+      if (t == 0)
+        vm_wait_tie<(W / 2 < W - 2 ? W / 2 : W - 2), STEPS>(a);
+      else if (t == 1)
+        wait_vmcnt<(W / 2 < W - 4 ? W / 2 : (W >= 4 ? W - 4 : 0))>();
+      else if (t == 2)
+        wait_vmcnt<(W >= 6 ? W - 6 : 0)>();
+      else
+        wait_vmcnt<0>();
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        const int blk = 2 * t + (q >> 1), slot = 32 * (q & 1) + 16 * cb + c;
+        const u32x4 wv = *reinterpret_cast<const u32x4*>(ws + blk * 1024 + slot * 16);
+        const float sc = e8m0_to_f32(ss[blk * 64 + slot]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          acc[cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a[t][s]), operand_from_word(wv[s], sc), acc[cb]);
+      }
+    }
+  } else {
+    const int i_c = c / CPD, rr_c = c % CPD;
+    const int rot_c = chunk_rot<KW>(i_c, rr_c);
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      if (cb == 0)
+        vm_wait_tie<NI, STEPS>(a);  // block 0's weights, scales and activations
+      else
+        wait_vmcnt<0>();
+      // this wave's CH scale bytes of the column: byte j scales chunk j
+      uint32_t scw[STEPS];
+      if constexpr (STEPS == 2) {
+        const u32x2 v2 = *reinterpret_cast<const u32x2*>(ss + (16 * cb + c) * CH);
+        scw[0] = v2.x;
+        scw[1] = v2.y;
+      } else {
+        const u32x4 v4 = *reinterpret_cast<const u32x4*>(ss + (16 * cb + c) * CH);
+        scw[0] = v4.x;
+        scw[1] = v4.y;
+        scw[2] = v4.z;
+        scw[3] = v4.w;
+      }
+#pragma unroll
+      for (int t = 0; t < STEPS; ++t) {
+        const int j = 4 * t + q;
+        const u32x4 wv = *reinterpret_cast<const u32x4*>(ws + (NI * cb + i_c) * 1024 + rr_c * (KW / 2) +
+                                                         16 * ((j + rot_c) & (CH - 1)));
+        const float sc = e8m0_to_f32(scw[t] >> (8 * q));
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          acc[cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a[t][s]), operand_from_word(wv[s], sc), acc[cb]);
+      }
+    }
+  }
+
+  // partial tile of this wave -> its own slot (its weights are consumed), then
+  // the sum over waves in wave order
+  float* const part = reinterpret_cast<float*>(ws);
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[(4 * q + i) * 32 + 16 * cb + c] = acc[cb][i];
+  __syncthreads();
+  // 128 groups of 4 outputs; a one-wave CTA (K = KW) takes two each
+  for (int e4 = threadIdx.x; e4 < 128; e4 += blockDim.x) {
+    const int e = 4 * e4;  // row e / 32, columns e % 32 .. +3 of the group
+    const int row = e >> 5, col = g * 32 + (e & 31);
+    if (row >= M) break;
+    f32x4 sum = *reinterpret_cast<const f32x4*>(smem + 4 * e);
+    for (int w = 1; w < nw; ++w) sum += *reinterpret_cast<const f32x4*>(smem + w * SLOT + 4 * e);
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = p.ep.any ? epilogue_value(p.ep, sum[i], row, col + i, N) : sum[i];
+    if (p.out_bf16) {
+      uint16_t* out = static_cast<uint16_t*>(p.C) + (size_t)row * N + col;
+      if ((N & 3) == 0 && col + 3 < N) {
+        *reinterpret_cast<u32x2*>(out) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (col + i < N) out[i] = (uint16_t)bf16_bits_rne(v[i]);
+      }
+    } else {
+      float* out = static_cast<float*>(p.C) + (size_t)row * N + col;
+      if ((N & 3) == 0 && col + 3 < N) {
+        *reinterpret_cast<f32x4*>(out) = f32x4{v[0], v[1], v[2], v[3]};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (col + i < N) out[i] = v[i];
+      }
+    }
+  }
+}
+
+template <int KW>
+hipError_t launch_whole(int layout, const StreamArgs& a, hipStream_t stream) {
+  if (a.M > 16 || a.K % KW != 0 || a.K / KW > WholeCfg<KW>::MAXW) return hipErrorInvalidValue;
+  const dim3 block(64 * (a.K / KW));
+  if (layout == kLayoutNK)
+    hipLaunchKernelGGL((stream_whole_kernel<kLayoutNK, KW>), dim3(a.groups), block, 0, stream, a);
+  else if (layout == kLayoutP)
+    hipLaunchKernelGGL((stream_whole_kernel<kLayoutP, KW>), dim3(a.groups), block, 0, stream, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 template <int MT, int WAVES, int GCB, int NSLOT, int SMAX, int KW>
 hipError_t launch_one(int layout, const StreamArgs& a, hipStream_t stream) {
   using Cfg = StreamCfg<MT, WAVES, GCB, NSLOT, KW>;
@@ -557,7 +797,15 @@ hipError_t launch_one(int layout, const StreamArgs& a, hipStream_t stream) {
 
 }  // namespace
 
+// The whole-K kernel's shapes: (1, 16, 2, 1, 1, KW) -- one unit per CTA, no ring
+// reuse, no split.
+bool whole_shape(const StreamShape& s) {
+  return s.mt == 1 && s.waves == WholeCfg<512>::MAXW && s.gcb == 2 && s.nslot == 1 && s.smax == 1 &&
+         (s.kw == 256 || s.kw == 512);
+}
+
 bool stream_shape_available(const StreamShape& s) {
+  if (whole_shape(s)) return true;
 #define X(MT_, W_, GCB_, NS_, SM_, KW_)                                                              \
   if (s.mt == MT_ && s.waves == W_ && s.gcb == GCB_ && s.nslot == NS_ && s.smax == SM_ && s.kw == KW_) \
     return true;
@@ -567,6 +815,10 @@ bool stream_shape_available(const StreamShape& s) {
 }
 
 hipError_t launch_stream(int layout, const StreamShape& s, const StreamArgs& args, hipStream_t stream) {
+  if (whole_shape(s)) {
+    if (args.splits != 1) return hipErrorInvalidValue;
+    return s.kw == 512 ? launch_whole<512>(layout, args, stream) : launch_whole<256>(layout, args, stream);
+  }
 #define X(MT_, W_, GCB_, NS_, SM_, KW_)                                                               \
   if (s.mt == MT_ && s.waves == W_ && s.gcb == GCB_ && s.nslot == NS_ && s.smax == SM_ && s.kw == KW_) \
     return launch_one<MT_, W_, GCB_, NS_, SM_, KW_>(layout, args, stream);

@@ -117,6 +117,7 @@ class StrategyDesc:
 #  * tiled-sched: dit_up 0.54, 70B FFN M=2048..8192 0.58 (plan variant 15);
 #  * tiled-pipe: dit_up 0.52 ([K/2,N]), 0.40 ([N,K/2]) (plan variant 6);
 #  * stream: decode M=16 N=K=8192 [N,K/2] 2.69 TB/s, P layout 3.03 TB/s;
+#  * stream-whole: M=1 N=K=8192 [N,K/2] 3.37 TB/s (P 3.59), N=28672 3.87 TB/s;
 #  * gemv: [K/2,N] decode 2.15 TB/s at N=8192, 3.56 TB/s at N=28672.
 STRATEGIES = (
     # 64 x 128 per wave: 4 A reads (1 KB) + 8 raw B words (256 B) per 32 MFMAs
@@ -126,6 +127,8 @@ STRATEGIES = (
     StrategyDesc("tiled-pipe", 256, 256, 64, 122, 0, dequant_overlap=1.0, achievable_eff=0.52,
                  converts_per_b=4.0, lds_bytes_per_mfma=192),
     StrategyDesc("stream", 16, 32, 512, 140, 0, dequant_overlap=1.0, achievable_eff=0.10, hbm_eff=0.34),
+    # one CTA per 32 columns x the whole K (M <= 8 in the C++ selector)
+    StrategyDesc("stream-whole", 16, 32, 8192, 136, 0, dequant_overlap=1.0, achievable_eff=0.10, hbm_eff=0.42),
     StrategyDesc("gemv", 16, 128, 32, 8, 0, dequant_overlap=1.0, achievable_eff=0.10, hbm_eff=0.30),
     # dequantize to a bf16 scratch, then a bf16 GEMM (the reference's strategy A)
     StrategyDesc("two-pass", 128, 256, 64, 0, 2, dequant_overlap=0.0, achievable_eff=0.60,

@@ -89,7 +89,8 @@ def test_epilogue_gemv(kk, layout, plan):
     check(kk, 16, 512, 2048, layout, plan, seed=1)
 
 
-@pytest.mark.parametrize("layout,plan", [("nk", (4, 3, 2)), ("p", (4, 0, 4)), ("nk", (4, 2, 1))])
+@pytest.mark.parametrize("layout,plan", [("nk", (4, 3, 2)), ("p", (4, 0, 4)), ("nk", (4, 2, 1)),
+                                         ("nk", (4, 5, 1)), ("p", (4, 6, 1))])
 def test_epilogue_stream(kk, layout, plan):
     M = 32 if plan[1] == 2 else 16
     K = 8192 if plan[2] > 1 else 1024

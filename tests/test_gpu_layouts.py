@@ -163,6 +163,23 @@ def test_stream_panels_equal_nk(kk, variant, mmax, kr, kw):
                 assert mo.strict_violations(a, ref, K) == 0
 
 
+@pytest.mark.parametrize("variant,kw,kmax", [(5, 512, 8192), (6, 256, 4096)])
+def test_stream_whole_panels_equal_nk(kk, variant, kw, kmax):
+    import torch
+
+    for M in (1, 16):
+        for N, K in ((512, kw), (992, 3 * kw), (4096, kmax)):
+            log(f"case stream-whole p vs nk variant={variant} M={M} N={N} K={K}")
+            A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=M + N + K + 3)
+            ref = oracle_f64(A_bits, W, S)
+            plan = (kk.KERNEL_STREAM, variant, 1)
+            for dt in (torch.float32, torch.bfloat16):
+                a = run_gemm(kk, A_bits, W, S, "p", dt, plan=plan)
+                b = run_gemm(kk, A_bits, W, S, "nk", dt, plan=plan)
+                assert np.array_equal(a, b), f"M={M} N={N} K={K} {dt}"
+                assert mo.strict_violations(a, ref, K) == 0
+
+
 @pytest.mark.parametrize("M", [1, 16, 32])
 def test_auto_plans_on_prepacked_decode_shapes(kk, M):
     """Decode shapes through the auto plan: P streams, G runs the tiled kernel

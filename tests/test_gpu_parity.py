@@ -220,6 +220,43 @@ def test_stream_variants(kk, variant, mmax, kr, kw):
                 assert bad == 0, f"M={M} N={N} K={K} {dt}: {bad} bad"
 
 
+# (variant, K per wave, largest K = 16 waves)
+WHOLE_VARIANTS = [(5, 512, 8192), (6, 256, 4096)]
+
+
+@pytest.mark.parametrize("variant,kw,kmax", WHOLE_VARIANTS)
+def test_stream_whole_variants(kk, variant, kw, kmax):
+    """Whole-K streaming kernel ([N,K/2], M <= 16): one wave (K = kw) up to
+    16 waves (K = kmax), ragged M, N % 32 != 0 and odd N (element stores),
+    fp32 and bf16 out; repeat calls are bitwise identical and bf16 out is the
+    fp32 result rounded."""
+    import torch
+
+    for M in (1, 7, 16):
+        for N, K in ((512, kw), (1000, 3 * kw), (1001, 2 * kw), (4096, kmax), (96, kmax)):
+            log(f"case stream-whole variant={variant} M={M} N={N} K={K}")
+            A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=M + N + K + 7)
+            ref = oracle_f64(A_bits, W, S)
+            plan = (kk.KERNEL_STREAM, variant, 1)
+            out = run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan)
+            bad = mo.strict_violations(out, ref, K)
+            assert bad == 0, f"M={M} N={N} K={K}: {bad} bad"
+            again = run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan)
+            assert np.array_equal(out, again), f"M={M} N={N} K={K}: not deterministic"
+            out16 = run_gemm(kk, A_bits, W, S, "nk", torch.bfloat16, plan=plan)
+            assert np.array_equal(out16, mo.bf16_bits_to_f32(mo.f32_to_bf16_bits(out))), f"M={M} N={N} K={K}"
+
+
+@pytest.mark.parametrize("variant,kw,kmax", WHOLE_VARIANTS)
+def test_stream_whole_rejects(kk, variant, kw, kmax):
+    import torch
+
+    for M, K, split in ((17, kw, 1), (16, kmax + kw, 1), (16, kmax + kw, 2), (16, kw + 32, 1)):
+        A_bits, W, S = mo.make_inputs(M, 64, K, 120, 132, seed=4)
+        with pytest.raises(RuntimeError, match="invalid argument"):  # M > 16, K > 16 waves, K % kw
+            run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=(kk.KERNEL_STREAM, variant, split))
+
+
 def test_stream_rejects_unsupported(kk):
     import torch
 
