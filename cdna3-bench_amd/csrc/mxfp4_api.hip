@@ -24,8 +24,9 @@ constexpr double kMfmaFlopsPerS = 2.5e15;
 constexpr double kLaunchS = 2.0e-6;  // fixed per-launch cost folded into every plan
 
 // Tiled kernel families: the first version (mxfp4_tiled.hip), the pipelined
-// kernel (mxfp4_tiled_pipe.hip) and the hand-scheduled 256 x 256 kernel
-// (mxfp4_tiled_sched.hip, [K/2,N] weights, K % 64 == 0).
+// kernel (mxfp4_tiled_pipe.hip) and the hand-scheduled 128 x 256 kernel
+// (mxfp4_tiled_sched.hip; [K/2,N] weights with K % 64 == 0, [N,K/2] with
+// K % 128 == 0).
 constexpr int kFamilyPlain = 0, kFamilyPipe = 1, kFamilySched = 2;
 
 struct TiledVariant {
@@ -58,7 +59,7 @@ const TiledVariant kTiled[] = {
     {{2, 4, 2, 2, 4}, 0.31, 0.26, 1, kFamilyPipe},  // 12: pipelined 128 x 256, 8 waves of 64 x 64
     {{1, 4, 4, 2, 4}, 0.32, 0.25, 1, kFamilyPipe},  // 13: pipelined 128 x 256, 4 waves of 128 x 64
     {{2, 1, 2, 4, 4}, 0.28, 0.24, 2, kFamilyPipe},  // 14: pipelined 128 x 128, 2 waves
-    {{2, 2, 2, 4, 3}, 0.55, 0.0, 2, kFamilySched}, // 15: hand-scheduled 128 x 256, 4 waves of 64 x 128, 2 CTAs / CU
+    {{2, 2, 2, 4, 3}, 0.55, 0.52, 2, kFamilySched}, // 15: hand-scheduled 128 x 256, 4 waves of 64 x 128, 2 CTAs / CU
 };
 constexpr int kNumTiled = sizeof(kTiled) / sizeof(kTiled[0]);
 
@@ -183,7 +184,8 @@ double tiled_eff(const TiledVariant& v, int layout) {
 // in the pipelined kernel, whose [N,K/2] loader reads aligned scale dwords.
 bool tiled_variant_ok(const TiledVariant& v, int layout, int64_t K) {
   if (v.family == kFamilyPlain) return layout == kLayoutKN || layout == kLayoutNK;
-  if (v.family == kFamilySched) return K % 64 == 0 && tiled_sched_available(layout, v.shape);
+  if (v.family == kFamilySched)
+    return K % (layout == kLayoutNK ? 128 : 64) == 0 && tiled_sched_available(layout, v.shape);
   if (layout == kLayoutNK) return K % 128 == 0;
   if (layout == kLayoutG) return v.shape.bn() % kGCols == 0;
   return true;

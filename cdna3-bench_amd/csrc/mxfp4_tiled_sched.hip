@@ -1,6 +1,8 @@
-// Hand-scheduled tiled MFMA kernel (M > 32, [K/2,N] weights, K % 64 == 0):
-// 128 x 256 x 64 tiles, 4 waves of 64 x 128, two CTAs per CU.  The production
-// kernel of the tiled family for the reference layout.
+// Hand-scheduled tiled MFMA kernel (M > 32; [K/2,N] weights with K % 64 == 0,
+// [N,K/2] weights with K % 128 == 0): 128 x 256 x 64 tiles, 4 waves of
+// 64 x 128, two CTAs per CU.  The production kernel of the tiled family for
+// both plain layouts; the layouts differ only in the B / scale loaders, the
+// B operand reads and the converts.
 //
 // Why it is built this way (measured on MI355X, dit_up 4096 x 12288 x 3072):
 //  * v_mfma_f32_16x16x32_bf16 sustains 1.68 PF/s (one wave per SIMD) and
@@ -33,14 +35,24 @@
 // this sub-step's operands 6, 7.  Raw words are therefore read one sub-step
 // ahead into a double buffer, A operands likewise.
 //
-// Stage in LDS (24.25 KB):
+// Stage in LDS ([K/2,N]: 24.25 KB, [N,K/2]: 25 KB):
 //   A  [128 rows][128 B]; 16-byte chunk c of row r at c ^ (r & 7) ^ ((r >> 3) & 1)
-//   B  [32 K-pair rows][256 B]; 16-byte chunk c of row R at c ^ 4 * ((R >> 2) & 3)
-//   S  [2 K groups][256 B] E8M0 scales of the stage's columns
+//   B  [K/2,N]: [32 K-pair rows][256 B]; 16-byte chunk c of row R at
+//      c ^ 4 * ((R >> 2) & 3)
+//      [N,K/2]: the 16-byte halves (K 0..31, 32..63 of the stage) of the 256
+//      columns; column 128w + 64g + 4c + j (c = 0..15) half h at byte
+//      4096w + 2048g + 512j + 32c + 16(h ^ (c >> 3)) -- each DMA moves 32 whole
+//      32-byte column segments, and the 16 columns of one operand read (fixed
+//      g, j, h) fill the 16 16-byte bank slots
+//   S  [K/2,N]: [2 K groups][256 B] E8M0 scales of the stage's columns
+//      [N,K/2]: [256 columns][4 B]: the column's scale dword of the stage pair
+//      (K groups 4u .. 4u+3 for stages 2u, 2u+1); a stage uses bytes
+//      2 (stage % 2) + 0, 1
 // MFMA v_mfma_f32_16x16x32_bf16: lane l holds A row l % 16, K 8(l / 16) .. +7
 // of the 32-K sub-step, and B column 4c + j of a 64-column group (c = l % 16,
-// MFMA j of the group): byte j of the four K-pair rows 4(l / 16) .. +3; the
-// result holds rows 4(l / 16) .. +3 of that column.
+// MFMA j of the group): [K/2,N] byte j of the four K-pair rows 4(l / 16) ..
+// +3, [N,K/2] word l / 16 of the column's half; the result holds rows
+// 4(l / 16) .. +3 of that column.
 //
 // Reference counterpart: the K loop of strategy_j / strategy_m
 // (csrc/strategy_j_synthesis.cu:120-170, csrc/strategy_m_asm.cu:131-185).
@@ -58,15 +70,23 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kRB = 4, kCB = 8;                 // 16-row x 16-column MFMA blocks per wave (64 x 128)
 constexpr int kABytes = kBM * kBK * 2;          // 16 KB
 constexpr int kBBytes = kBN * kBK / 2;          // 8 KB
-constexpr int kSBytes = 2 * kBN;                // 512 B
-constexpr int kStage = kABytes + kBBytes + kSBytes;
 constexpr int kNS = 3;                          // LDS ring depth
-constexpr int kLds = kNS * kStage + 256;        // + the window of the idle scale DMAs
 constexpr int kADma = kABytes / 1024 / kWaves;  // 4 per wave per stage
 constexpr int kBDma = kBBytes / 1024 / kWaves;  // 2
 constexpr int kVmPerStage = kADma + kBDma + 1;  // + one scale DMA
-static_assert(2 * kLds <= 160 * 1024, "two CTAs per CU");
 static_assert(2 * kVmPerStage < 64, "vmcnt range");
+
+// Per-layout LDS sizes: [K/2,N] stages hold 2 x 256 scale bytes (two of the
+// four waves move them; the other two DMA into a spare 256-byte window),
+// [N,K/2] stages 256 scale dwords (one DMA per wave).
+template <int L>
+struct SchedLds {
+  static constexpr int kSBytes = L == kLayoutKN ? 2 * kBN : 4 * kBN;
+  static constexpr int kStage = kABytes + kBBytes + kSBytes;
+  static constexpr int kLds = kNS * kStage + (L == kLayoutKN ? 256 : 0);
+  static_assert(kStage % 256 == 0, "slot offsets are ds_read2st64 immediates");
+  static_assert(2 * kLds <= 160 * 1024, "two CTAs per CU");
+};
 
 __device__ __forceinline__ int a_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
@@ -107,8 +127,8 @@ __device__ __forceinline__ void lgkm_wait() {
 }
 // The same wait, redefining w and x: compiler-scheduled code that reads them
 // (asm LDS reads' results) cannot move above it.
-template <int N>
-__device__ __forceinline__ void lgkm_wait(u32x2& w, u32x2& x) {
+template <int N, typename T>
+__device__ __forceinline__ void lgkm_wait(T& w, T& x) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(w), "+v"(x) : "i"(N));
 }
 template <int N>
@@ -138,9 +158,12 @@ __device__ __forceinline__ float e8m0_byte(uint32_t w, int j) {
 // instantiation per store kind: with all three store loops in one kernel the
 // register allocator spills accumulators before the branch, so even the plain
 // stores went through scratch.
-template <int kOut>
-__global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
+template <int L, int kOut>
+__global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
+  static_assert(L == kLayoutKN || L == kLayoutNK, "plain layouts");
+  constexpr bool kKN = L == kLayoutKN;
+  constexpr int kStage = SchedLds<L>::kStage;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SchedLds<L>::kLds];
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
   const int lane = threadIdx.x & 63;
@@ -167,8 +190,9 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
 
   // ---- loop-invariant DMA offsets (the K step goes in soffset) ---------------
   const desc_t dA = make_desc(p.A + (size_t)m0 * K);
-  const desc_t dB = make_desc(p.B + n0);
-  const desc_t dS = make_desc(p.S + n0);
+  const int G = K / 32;
+  const desc_t dB = make_desc(kKN ? p.B + n0 : p.B + (size_t)n0 * (K / 2));
+  const desc_t dS = make_desc(kKN ? p.S + n0 : p.S + (size_t)n0 * G);
   const desc_t dNull = make_desc(p.A, 0u);  // every lane out of range: writes zeros
   uint32_t va[kADma];                       // A: DMA i covers rows 8i .. 8i+7
 #pragma unroll
@@ -178,19 +202,36 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
     const int lc = (lane & 7) ^ a_swz(row);
     va[ii] = m0 + row < M ? (uint32_t)(row * K * 2 + lc * 16) : kOobOffset;
   }
-  uint32_t vb[kBDma];                       // B: DMA i covers K-pair rows 4i .. 4i+3
+  uint32_t vb[kBDma];
 #pragma unroll
   for (int ii = 0; ii < kBDma; ++ii) {
-    const int qq = (wave * kBDma + ii) * 64 + lane;
-    const int row = qq >> 4;
-    const int lc = (qq & 15) ^ (4 * ((row >> 2) & 3));
-    vb[ii] = n0 + lc * 16 < N ? (uint32_t)(row * N + lc * 16) : kOobOffset;
+    const int d = wave * kBDma + ii;
+    if constexpr (kKN) {
+      // DMA d covers K-pair rows 4d .. 4d+3
+      const int qq = d * 64 + lane;
+      const int row = qq >> 4;
+      const int lc = (qq & 15) ^ (4 * ((row >> 2) & 3));
+      vb[ii] = n0 + lc * 16 < N ? (uint32_t)(row * N + lc * 16) : kOobOffset;
+    } else {
+      // DMA d = 4w + 2g + j/2 covers columns 128w + 64g + 4c + j (c = 0..15,
+      // j = 2 (d % 2) + cl / 16) of lane pair cl = lane / 2; lane bit h' is
+      // half h' ^ (c >> 3) of its column
+      const int cl = lane >> 1, cc = cl & 15;
+      const int col = 128 * (d >> 2) + 64 * ((d >> 1) & 1) + 4 * cc + 2 * (d & 1) + (cl >> 4);
+      const int half = (lane & 1) ^ (cc >> 3);
+      vb[ii] = n0 + col < N ? (uint32_t)(col * (K / 2) + 16 * half) : kOobOffset;
+    }
   }
-  // scales: waves 0, 1 move K group rows 0, 1 of the stage (256 columns each);
-  // waves 2, 3 issue the same DMA into a spare window so every wave counts
-  // the same number of loads per stage.
-  const bool sc_wave = wave < 2;
-  const uint32_t vs = sc_wave && n0 + 4 * lane < N ? (uint32_t)(wave * N + 4 * lane) : kOobOffset;
+  // scales, [K/2,N]: waves 0, 1 move K group rows 0, 1 of the stage (256
+  // columns each); waves 2, 3 issue the same DMA into a spare window so every
+  // wave counts the same number of loads per stage.  [N,K/2]: wave w moves
+  // the stage pair's dword of columns 64w .. 64w+63.
+  const bool sc_wave = !kKN || wave < 2;
+  uint32_t vs;
+  if constexpr (kKN)
+    vs = sc_wave && n0 + 4 * lane < N ? (uint32_t)(wave * N + 4 * lane) : kOobOffset;
+  else
+    vs = n0 + 64 * wave + lane < N ? (uint32_t)((64 * wave + lane) * G) : kOobOffset;
   const uint32_t sc_lds = sc_wave ? (uint32_t)(kABytes + kBBytes + 256 * wave) : 0u;
 
   auto issue_a = [&](int ii, int slot, int step, bool live) __attribute__((always_inline)) {
@@ -199,11 +240,11 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
   };
   auto issue_b = [&](int ii, int slot, int step, bool live) __attribute__((always_inline)) {
     dma16s(live ? dB : dNull, lds0 + slot * kStage + kABytes + (wave * kBDma + ii) * 1024, vb[ii],
-           (uint32_t)step * (kBK / 2) * (uint32_t)N);
+           kKN ? (uint32_t)step * (kBK / 2) * (uint32_t)N : (uint32_t)step * (kBK / 2));
   };
   auto issue_s = [&](int slot, int step, bool live) __attribute__((always_inline)) {
     dma4s(live ? dS : dNull, sc_wave ? lds0 + slot * kStage + sc_lds : lds0 + kNS * kStage, vs,
-          (uint32_t)step * 2u * (uint32_t)N);
+          kKN ? (uint32_t)step * 2u * (uint32_t)N : (uint32_t)(step >> 1) * 4u);
   };
   // DMA number d (0 .. kVmPerStage-1) of a stage
   auto issue_dma = [&](int d, int slot, int step, bool live) __attribute__((always_inline)) {
@@ -222,15 +263,24 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) a_off[sub] = lds0 + (uint32_t)(row * 128 + (((sub * 4 + q) ^ a_swz(row)) * 16));
   }
-  // B: K-pair row sub*16 + 4q + i, column byte wn*128 + 64g + 4c (group g);
-  // the row swizzle depends on q only.
+  // B, [K/2,N]: K-pair row sub*16 + 4q + i, column byte wn*128 + 64g + 4c
+  // (b_off[g]; the row swizzle depends on q only).  [N,K/2]: word q of half
+  // `sub` of column wn*128 + 64g + 4c + j (b_off[sub]; g, j are immediates).
   uint32_t b_off[2];
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const int colb = wn * 128 + 64 * g + 4 * c;
-    b_off[g] = lds0 + (uint32_t)(kABytes + 4 * q * kBN + (((colb >> 4) ^ (4 * q)) * 16) + (colb & 15));
+  for (int i = 0; i < 2; ++i) {
+    if constexpr (kKN) {
+      const int colb = wn * 128 + 64 * i + 4 * c;
+      b_off[i] = lds0 + (uint32_t)(kABytes + 4 * q * kBN + (((colb >> 4) ^ (4 * q)) * 16) + (colb & 15));
+    } else {
+      b_off[i] = lds0 + (uint32_t)(kABytes + 4096 * wn + 32 * c + 16 * (i ^ (c >> 3)) + 4 * q);
+    }
   }
-  const uint32_t s_off = lds0 + (uint32_t)(kABytes + kBBytes + wn * 128 + 4 * c);  // + 64 g
+  // scales: [K/2,N] bytes of columns wn*128 + 4c .. +3 (+ 64 g), [N,K/2] their
+  // dwords
+  const uint32_t s_off = kKN ? lds0 + (uint32_t)(kABytes + kBBytes + wn * 128 + 4 * c)
+                             : lds0 + (uint32_t)(kABytes + kBBytes + wn * 512 + 16 * c);
+  using ScaleWords = std::conditional_t<kKN, u32x2, u32x4>;
 
   f32x4 acc[kRB][kCB];
 #pragma unroll
@@ -245,18 +295,32 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
     float sc[2][kCB];    // scales per K group of the stage and block
 
     // LDS reads of ring slot SL (a compile-time constant: every address is a
-    // loop-invariant register plus an immediate offset; kStage = 98 x 256 B).
+    // loop-invariant register plus an immediate offset; kStage is a multiple
+    // of 256 B).  Raw word 4g + i: [K/2,N] K-pair row 4q + i of columns
+    // 4c .. +3, [N,K/2] column 4c + i (both of group g).
     auto read_raw = [&](auto slot_c, int sub, uint32_t (&r)[8]) __attribute__((always_inline)) {
       constexpr int O = decltype(slot_c)::value * (kStage / 256);
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
         u32x2 x, y;
-        if (sub == 0) {
-          x = lds_2st64<O + 0, O + 1>(b_off[g]);
-          y = lds_2st64<O + 2, O + 3>(b_off[g]);
+        if constexpr (kKN) {
+          if (sub == 0) {
+            x = lds_2st64<O + 0, O + 1>(b_off[g]);
+            y = lds_2st64<O + 2, O + 3>(b_off[g]);
+          } else {
+            x = lds_2st64<O + 16, O + 17>(b_off[g]);
+            y = lds_2st64<O + 18, O + 19>(b_off[g]);
+          }
         } else {
-          x = lds_2st64<O + 16, O + 17>(b_off[g]);
-          y = lds_2st64<O + 18, O + 19>(b_off[g]);
+          // columns j are 512 B apart, groups 2048 B
+          const uint32_t base = b_off[sub];
+          if (g == 0) {
+            x = lds_2st64<O + 0, O + 2>(base);
+            y = lds_2st64<O + 4, O + 6>(base);
+          } else {
+            x = lds_2st64<O + 8, O + 10>(base);
+            y = lds_2st64<O + 12, O + 14>(base);
+          }
         }
         r[4 * g + 0] = x.x; r[4 * g + 1] = x.y; r[4 * g + 2] = y.x; r[4 * g + 3] = y.y;
       }
@@ -269,26 +333,55 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
       o[2] = lds_b128<O + 4096>(addr);
       o[3] = lds_b128<O + 6144>(addr);
     };
-    // scale words: w = (K group 0, 1) of column group 0, x = of column group 1
-    auto read_scales = [&](auto slot_c, u32x2& w, u32x2& x) __attribute__((always_inline)) {
-      constexpr int O = decltype(slot_c)::value * (kStage / 256);
-      w = lds_2st64<O, O + 1>(s_off);
-      x = lds_2st64<O, O + 1>(s_off + 64);
+    // scale words of column group 0 (w) and 1 (x): [K/2,N] K group 0, 1;
+    // [N,K/2] the dwords of columns 4c + j
+    auto read_scales = [&](auto slot_c, ScaleWords& w, ScaleWords& x) __attribute__((always_inline)) {
+      if constexpr (kKN) {
+        constexpr int O = decltype(slot_c)::value * (kStage / 256);
+        w = lds_2st64<O, O + 1>(s_off);
+        x = lds_2st64<O, O + 1>(s_off + 64);
+      } else {
+        constexpr int O = decltype(slot_c)::value * kStage;
+        w = __builtin_bit_cast(u32x4, lds_b128<O>(s_off));
+        x = __builtin_bit_cast(u32x4, lds_b128<O + 256>(s_off));
+      }
     };
-    auto scales_from = [&](u32x2 w, u32x2 x) __attribute__((always_inline)) {
+    // step: the absolute K step of the scales ([N,K/2]: its parity picks the
+    // half of the stage pair's dword)
+    auto scales_from = [&](ScaleWords w, ScaleWords x, int step) __attribute__((always_inline)) {
+      if constexpr (kKN) {
+        (void)step;
 #pragma unroll
-      for (int kg = 0; kg < 2; ++kg)
+        for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            sc[kg][j] = e8m0_byte(kg ? w.y : w.x, j);
+            sc[kg][4 + j] = e8m0_byte(kg ? x.y : x.x, j);
+          }
+      } else {
+        const uint32_t sh = 16u * (uint32_t)(step & 1);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          sc[kg][j] = e8m0_byte(kg ? w.y : w.x, j);
-          sc[kg][4 + j] = e8m0_byte(kg ? x.y : x.x, j);
+          const uint32_t h0 = w[j] >> sh, h1 = x[j] >> sh;
+          sc[0][j] = e8m0_byte(h0, 0);
+          sc[1][j] = e8m0_byte(h0, 1);
+          sc[0][4 + j] = e8m0_byte(h1, 0);
+          sc[1][4 + j] = e8m0_byte(h1, 1);
         }
+      }
     };
     // the four converts of B operand cb (= 4g + j) from raw words r
     auto convert = [&](int cb, const uint32_t (&r)[8], float s) __attribute__((always_inline)) {
       const int g = cb >> 2, j = cb & 3;
       const uint32_t* w = r + 4 * g;
       u32x4 v;
+      if constexpr (!kKN) {
+        // one word: K pairs 4q .. 4q+3 of column 4c + j
+        const uint32_t x = r[cb];
+        v = u32x4{cvt_fp4<0>(x, s), cvt_fp4<1>(x, s), cvt_fp4<2>(x, s), cvt_fp4<3>(x, s)};
+        b[cb] = __builtin_bit_cast(bf16x8, v);
+        return;
+      }
       switch (j) {
         case 0: v = u32x4{cvt_fp4<0>(w[0], s), cvt_fp4<0>(w[1], s), cvt_fp4<0>(w[2], s), cvt_fp4<0>(w[3], s)}; break;
         case 1: v = u32x4{cvt_fp4<1>(w[0], s), cvt_fp4<1>(w[1], s), cvt_fp4<1>(w[2], s), cvt_fp4<1>(w[3], s)}; break;
@@ -306,12 +399,12 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
     vm_wait<(kNS - 1) * kVmPerStage>();
     barrier_asm();
     {
-      u32x2 w, x;
+      ScaleWords w, x;
       read_scales(std::integral_constant<int, 0>{}, w, x);
       read_raw(std::integral_constant<int, 0>{}, 0, raw[0]);
       read_a(std::integral_constant<int, 0>{}, 0, a[0]);
       lgkm_wait<0>(w, x);
-      scales_from(w, x);
+      scales_from(w, x, s_begin);
 #pragma unroll
       for (int cb = 0; cb < kCB; ++cb) convert(cb, raw[0], sc[0][cb]);
     }
@@ -325,7 +418,7 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         const int pc = sub, pn = sub ^ 1;  // raw / A buffers of this and the next sub-step
-        u32x2 w = {0u, 0u}, x = {0u, 0u};
+        ScaleWords w{}, x{};
         if (sub == 0) {
           read_raw(slot_c, 1, raw[pn]);
           read_a(slot_c, 1, a[pn]);
@@ -357,7 +450,7 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
             } else {
               lgkm_wait<kRB>(w, x);
               convert(7, raw[pc], sc[1][7]);
-              scales_from(w, x);  // stage t's scales are dead from here
+              scales_from(w, x, s_begin + t + 1);  // stage t's scales are dead from here
             }
           } else if (cb == 0) {
             convert(6, raw[pc], sc[sub][6]);
@@ -445,18 +538,29 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kn_kernel(TiledArgs p
 }  // namespace
 
 bool tiled_sched_available(int layout, const TiledShape& s) {
-  return layout == kLayoutKN && s.bm() == kBM && s.bn() == kBN && s.wm * s.wn == kWaves && s.stages == kNS;
+  return (layout == kLayoutKN || layout == kLayoutNK) && s.bm() == kBM && s.bn() == kBN &&
+         s.wm * s.wn == kWaves && s.stages == kNS;
+}
+
+template <int L>
+void launch_sched_layout(const TiledArgs& args, int grid, hipStream_t stream) {
+  if (args.ep.any)
+    hipLaunchKernelGGL((tiled_sched_kernel<L, 2>), dim3(grid), dim3(kThreads), 0, stream, args);
+  else if (args.out_bf16)
+    hipLaunchKernelGGL((tiled_sched_kernel<L, 1>), dim3(grid), dim3(kThreads), 0, stream, args);
+  else
+    hipLaunchKernelGGL((tiled_sched_kernel<L, 0>), dim3(grid), dim3(kThreads), 0, stream, args);
 }
 
 hipError_t launch_tiled_sched(int layout, const TiledShape& shape, const TiledArgs& args, hipStream_t stream) {
-  if (!tiled_sched_available(layout, shape) || args.K % kBK != 0) return hipErrorInvalidValue;
+  // [N,K/2] reads each column's scales as aligned dwords of K-step pairs
+  const int kmod = layout == kLayoutKN ? kBK : 2 * kBK;
+  if (!tiled_sched_available(layout, shape) || args.K % kmod != 0) return hipErrorInvalidValue;
   const int grid = args.tiles_m * args.tiles_n * args.splits;
-  if (args.ep.any)
-    hipLaunchKernelGGL(tiled_sched_kn_kernel<2>, dim3(grid), dim3(kThreads), 0, stream, args);
-  else if (args.out_bf16)
-    hipLaunchKernelGGL(tiled_sched_kn_kernel<1>, dim3(grid), dim3(kThreads), 0, stream, args);
+  if (layout == kLayoutKN)
+    launch_sched_layout<kLayoutKN>(args, grid, stream);
   else
-    hipLaunchKernelGGL(tiled_sched_kn_kernel<0>, dim3(grid), dim3(kThreads), 0, stream, args);
+    launch_sched_layout<kLayoutNK>(args, grid, stream);
   return hipGetLastError();
 }
 

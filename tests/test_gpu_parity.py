@@ -123,7 +123,7 @@ def test_generic_kernel_odd_n(kk):
 
 TILED_VARIANTS = range(16)
 PIPE_VARIANTS = range(6, 15)  # pipelined kernel; [N,K/2] needs K % 128 == 0
-SCHED_VARIANT = 15            # hand-scheduled kernel: [K/2,N] and K % 64 == 0 only
+SCHED_VARIANT = 15            # hand-scheduled kernel: [K/2,N] with K % 64 == 0, [N,K/2] with K % 128 == 0
 GEMV_VARIANTS = range(15)
 
 
@@ -139,7 +139,7 @@ def test_every_tiled_variant_and_split(kk, layout, K):
             log(f"case tiled variant={v} split={split} layout={layout} K={K}")
             plan = (kk.KERNEL_TILED, v, split)
             if (layout == "nk" and K % 128 and v in PIPE_VARIANTS) or (
-                    v == SCHED_VARIANT and (layout != "kn" or K % 64)):
+                    v == SCHED_VARIANT and K % (64 if layout == "kn" else 128)):
                 with pytest.raises(RuntimeError, match="invalid argument"):
                     run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=plan)
                 continue
@@ -148,12 +148,14 @@ def test_every_tiled_variant_and_split(kk, layout, K):
             assert bad == 0, f"variant {v} split {split}: {bad} bad"
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 528, 640), (64, 256, 64), (513, 1040, 1536)])
-def test_sched_kernel_tails_and_splits(kk, M, N, K):
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("M,N,K", [(300, 528, 640), (64, 256, 128), (513, 1040, 1536)])
+def test_sched_kernel_tails_and_splits(kk, layout, M, N, K):
     """Hand-scheduled kernel: M / N tails (N % 256 != 0), splits down to one
-    64-K step, fp32 and bf16 out, against the float64 oracle; every split
-    count sums the same 64-K partial products (fp32), so splits agree to
-    within fp32 reassociation, and bf16 out is the fp32 result rounded."""
+    64-K step (odd first steps: the [N,K/2] scale dword half), fp32 and bf16
+    out, against the float64 oracle; every split count sums the same 64-K
+    partial products (fp32), so splits agree to within fp32 reassociation,
+    and bf16 out is the fp32 result rounded."""
     import torch
 
     A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=33)
@@ -161,12 +163,12 @@ def test_sched_kernel_tails_and_splits(kk, M, N, K):
     plan = lambda split: (kk.KERNEL_TILED, SCHED_VARIANT, split)
     base = None
     for split in sorted({s for s in (1, 2, 3, K // 64) if s <= K // 64}):
-        log(f"case sched M={M} N={N} K={K} split={split}")
-        out = run_gemm(kk, A_bits, W, S, "kn", torch.float32, plan=plan(split))
+        log(f"case sched {layout} M={M} N={N} K={K} split={split}")
+        out = run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=plan(split))
         assert mo.strict_violations(out, ref, K) == 0, f"split {split}"
-        again = run_gemm(kk, A_bits, W, S, "kn", torch.float32, plan=plan(split))
+        again = run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=plan(split))
         assert np.array_equal(out, again), f"split {split}: not deterministic"
-        out16 = run_gemm(kk, A_bits, W, S, "kn", torch.bfloat16, plan=plan(split))
+        out16 = run_gemm(kk, A_bits, W, S, layout, torch.bfloat16, plan=plan(split))
         assert np.array_equal(out16, mo.bf16_bits_to_f32(mo.f32_to_bf16_bits(out))), f"split {split}: bf16 rounding"
         if base is None:
             base = out
