@@ -602,7 +602,9 @@ __global__ void __launch_bounds__(1024, 1) stream_whole_kernel(StreamArgs p) {
   // loads (L2 hits, 16 rows x KW x 2 bytes per wave -- twice the wave's
   // weight bytes at M = 16) are taken in while those stream, and the first
   // half's compute waits only for them.
-  // activations: lane (c, q) holds row c, K kw0 + 128t + 32q + 8s .. +7 in a[t][s]
+  // activations: lane (c, q) holds row c, K kw0 + 128t + 32s + 8q .. +7 in
+  // a[t][s] (MFMA (t, s) of the wave's range: the four lanes of a row read 64
+  // contiguous bytes per load); the weights are read in the same K order
   u32x4 a[STEPS][4];
   auto issue_a = [&]() __attribute__((always_inline)) {
     const desc_t d = make_desc(p.A);
@@ -610,7 +612,7 @@ __global__ void __launch_bounds__(1024, 1) stream_whole_kernel(StreamArgs p) {
     for (int t = 0; t < STEPS; ++t)
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        a[t][s] = asm_load16(d, c < M ? (uint32_t)((c * K + kw0 + 128 * t + 32 * q + 8 * s) * 2) : kOobOffset);
+        a[t][s] = asm_load16(d, c < M ? (uint32_t)((c * K + kw0 + 128 * t + 32 * s + 8 * q) * 2) : kOobOffset);
   };
   if constexpr (LAYOUT == kLayoutP) {
     // scales: KW/64 blocks of 64 bytes; weights: KW/64 blocks of 1 KB, both
@@ -675,12 +677,14 @@ __global__ void __launch_bounds__(1024, 1) stream_whole_kernel(StreamArgs p) {
         wait_vmcnt<0>();
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
-        const int blk = 2 * t + (q >> 1), slot = 32 * (q & 1) + 16 * cb + c;
-        const u32x4 wv = *reinterpret_cast<const u32x4*>(ws + blk * 1024 + slot * 16);
-        const float sc = e8m0_to_f32(ss[blk * 64 + slot]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          acc[cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a[t][s]), operand_from_word(wv[s], sc), acc[cb]);
+        for (int s = 0; s < 4; ++s) {
+          // chunk 4t + s = block 2t + s/2, lane slot 32 (s % 2) + column; word q
+          const int blk = 2 * t + (s >> 1), slot = 32 * (s & 1) + 16 * cb + c;
+          const uint32_t w = *reinterpret_cast<const uint32_t*>(ws + blk * 1024 + slot * 16 + 4 * q);
+          const float sc = e8m0_to_f32(ss[blk * 64 + slot]);
+          acc[cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a[t][s]), operand_from_word(w, sc), acc[cb]);
+        }
       }
     }
   } else {
@@ -707,13 +711,15 @@ __global__ void __launch_bounds__(1024, 1) stream_whole_kernel(StreamArgs p) {
       }
 #pragma unroll
       for (int t = 0; t < STEPS; ++t) {
-        const int j = 4 * t + q;
-        const u32x4 wv = *reinterpret_cast<const u32x4*>(ws + (NI * cb + i_c) * 1024 + rr_c * (KW / 2) +
-                                                         16 * ((j + rot_c) & (CH - 1)));
-        const float sc = e8m0_to_f32(scw[t] >> (8 * q));
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          acc[cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a[t][s]), operand_from_word(wv[s], sc), acc[cb]);
+        for (int s = 0; s < 4; ++s) {
+          // word q of chunk 4t + s; its scale is byte s of scw[t]
+          const int j = 4 * t + s;
+          const uint32_t w = *reinterpret_cast<const uint32_t*>(ws + (NI * cb + i_c) * 1024 + rr_c * (KW / 2) +
+                                                                16 * ((j + rot_c) & (CH - 1)) + 4 * q);
+          const float sc = e8m0_to_f32(scw[t] >> (8 * s));
+          acc[cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a[t][s]), operand_from_word(w, sc), acc[cb]);
+        }
       }
     }
   }
