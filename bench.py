@@ -228,6 +228,15 @@ def main():
         },
     }
 
+    # the same workload with the other plain weight layout (the BASELINE
+    # configs store W as [N,K/2]; the reference extension takes [K/2,N])
+    other = "nk" if args.layout == "kn" else "kn"
+    up2 = measure(kk, UP, other, args.steps, args.warmup)
+    tf2 = flops / (up2["ms"] * 1e-3) / 1e12
+    result["other_layout"] = {"layout": other, "value": round(tf2, 2), "unit": "TFLOP/s",
+                              "pct_bf16_peak": round(100.0 * tf2 / PEAK_BF16_TFLOPS, 2),
+                              "ms_per_step": round(up2["ms"], 5), "plan": up2["plan"]}
+
     if not args.no_decode:
         dbytes = gemm_bytes(DECODE["M"], DECODE["N"], DECODE["K"])
         legs = {}
@@ -252,6 +261,15 @@ def main():
                           "plan": legs["kn"][0]["plan"],
                           "traffic": profile_traffic("gemv_decode_m16_kn")},
         }
+        # the other M of the BASELINE decode config ([N,K/2], N = K = 8192)
+        sweep = {}
+        for m in (1, 8, 32):
+            cfg = dict(DECODE, name=f"decode_m{m}", M=m)
+            d = measure(kk, cfg, "nk", max(args.steps, 200), args.warmup)
+            gb = gemm_bytes(m, cfg["N"], cfg["K"]) / (d["ms"] * 1e-3) / 1e9
+            sweep[f"M{m}"] = {"value": round(gb, 1), "unit": "GB/s", "pct_hbm_peak": round(100.0 * gb / PEAK_HBM_GBPS, 2),
+                              "us_per_step": round(d["ms"] * 1e3, 3), "plan": d["plan"]}
+        result["hbm_decode"]["m_sweep"] = sweep
 
     # the committed rocprof summary of the kernel the plan runs
     family = "tiled_sched" if up["plan"].startswith("tiled-sched") else "tiled"
