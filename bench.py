@@ -16,7 +16,7 @@ repeated for ~10 s with every host core (median reported).  roofline.traffic
 is read from the committed rocprofv3 summary of the same kernel and workload
 (profiles/<kernel>_<workload>.md: FETCH_SIZE + WRITE_SIZE, copy-calibrated).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout kn|nk]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout kn|nk|g]
                        [--no-cpu] [--no-decode] [--calibrate-copy]
 """
 
@@ -58,7 +58,12 @@ def make_inputs(cfg, layout, seed=0):
     S = rng.integers(cfg["exp_lo"], cfg["exp_hi"] + 1, (N, K // 32), dtype=np.uint8)
     if layout == "kn":
         W, S = np.ascontiguousarray(W.T), np.ascontiguousarray(S.T)
-    return A, torch.from_numpy(W).cuda(), torch.from_numpy(S).cuda()
+    W, S = torch.from_numpy(W).cuda(), torch.from_numpy(S).cuda()
+    if layout in ("g", "p"):  # the device prepack of the [N,K/2] weights
+        from mxfp4_cdna3 import kernels as kk
+
+        W, S = kk.convert_layout(W, S, "nk", layout)
+    return A, W, S
 
 
 def gemm_bytes(M, N, K, c_bytes=2):
@@ -173,7 +178,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--layout", choices=["kn", "nk"], default="kn")
+    ap.add_argument("--layout", choices=["kn", "nk", "g"], default="kn")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode HBM leg")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -212,7 +217,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded; E2M1 codes uniform, E8M0 120..132, A ~ N(0,1))",
         "config": {
-            "workload": f"dit_up M={M} N={N} K={K}, weights {'[K/2,N] (reference layout)' if args.layout == 'kn' else '[N,K/2]'}, bf16 out",
+            "workload": f"dit_up M={M} N={N} K={K}, weights "
+                        f"{ {'kn': '[K/2,N] (reference layout)', 'nk': '[N,K/2]', 'g': 'G (reference prepack)'}[args.layout] }, bf16 out",
             "M": M, "N": N, "K": K, "layout": args.layout, "plan": up["plan"],
             "rotation_sets": up["rotation_sets"], "timing": "hip graph of K launches, events",
         },
@@ -228,14 +234,17 @@ def main():
         },
     }
 
-    # the same workload with the other plain weight layout (the BASELINE
-    # configs store W as [N,K/2]; the reference extension takes [K/2,N])
-    other = "nk" if args.layout == "kn" else "kn"
-    up2 = measure(kk, UP, other, args.steps, args.warmup)
-    tf2 = flops / (up2["ms"] * 1e-3) / 1e12
-    result["other_layout"] = {"layout": other, "value": round(tf2, 2), "unit": "TFLOP/s",
-                              "pct_bf16_peak": round(100.0 * tf2 / PEAK_BF16_TFLOPS, 2),
-                              "ms_per_step": round(up2["ms"], 5), "plan": up2["plan"]}
+    # the same workload with the other weight layouts: [N,K/2] (the BASELINE
+    # configs store W so; the reference extension takes [K/2,N]) and G (the
+    # reference's prepack_b_mxfp4 format, prepacked outside the timed region
+    # as the reference's bench does for strategy G)
+    result["other_layouts"] = {}
+    for other in [l for l in ("kn", "nk", "g") if l != args.layout]:
+        up2 = measure(kk, UP, other, args.steps, args.warmup)
+        tf2 = flops / (up2["ms"] * 1e-3) / 1e12
+        result["other_layouts"][other] = {"value": round(tf2, 2), "unit": "TFLOP/s",
+                                          "pct_bf16_peak": round(100.0 * tf2 / PEAK_BF16_TFLOPS, 2),
+                                          "ms_per_step": round(up2["ms"], 5), "plan": up2["plan"]}
 
     if not args.no_decode:
         dbytes = gemm_bytes(DECODE["M"], DECODE["N"], DECODE["K"])

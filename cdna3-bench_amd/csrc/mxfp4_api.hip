@@ -25,8 +25,8 @@ constexpr double kLaunchS = 2.0e-6;  // fixed per-launch cost folded into every 
 
 // Tiled kernel families: the first version (mxfp4_tiled.hip), the pipelined
 // kernel (mxfp4_tiled_pipe.hip) and the hand-scheduled 128 x 256 kernel
-// (mxfp4_tiled_sched.hip; [K/2,N] weights with K % 64 == 0, [N,K/2] with
-// K % 128 == 0).
+// (mxfp4_tiled_sched.hip; [K/2,N] and G weights with K % 64 == 0, [N,K/2]
+// with K % 128 == 0).
 constexpr int kFamilyPlain = 0, kFamilyPipe = 1, kFamilySched = 2;
 
 struct TiledVariant {
@@ -180,8 +180,10 @@ double tiled_eff(const TiledVariant& v, int layout) {
   return layout == kLayoutKN || layout == kLayoutG ? v.eff_kn : v.eff_nk;
 }
 
-// Tiled variants a layout may use: the prepacked layouts only have loaders
-// in the pipelined kernel, whose [N,K/2] loader reads aligned scale dwords.
+// Tiled variants a layout may use: the first tiled kernel has only the plain
+// loaders, the scheduled kernel the plain and G ones ([N,K/2]: aligned scale
+// dwords of K-step pairs), the pipelined kernel all four (its [N,K/2] loader
+// reads aligned scale dwords).
 bool tiled_variant_ok(const TiledVariant& v, int layout, int64_t K) {
   if (v.family == kFamilyPlain) return layout == kLayoutKN || layout == kLayoutNK;
   if (v.family == kFamilySched)

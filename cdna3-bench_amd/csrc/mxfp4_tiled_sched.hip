@@ -1,8 +1,8 @@
-// Hand-scheduled tiled MFMA kernel (M > 32; [K/2,N] weights with K % 64 == 0,
-// [N,K/2] weights with K % 128 == 0): 128 x 256 x 64 tiles, 4 waves of
-// 64 x 128, two CTAs per CU.  The production kernel of the tiled family for
-// both plain layouts; the layouts differ only in the B / scale loaders, the
-// B operand reads and the converts.
+// Hand-scheduled tiled MFMA kernel (M > 32; [K/2,N] or G weights with
+// K % 64 == 0, [N,K/2] weights with K % 128 == 0): 128 x 256 x 64 tiles, 4
+// waves of 64 x 128, two CTAs per CU.  The production kernel of the tiled
+// family for these layouts; they differ only in the B / scale loaders, the B
+// operand reads and the converts.
 //
 // Why it is built this way (measured on MI355X, dit_up 4096 x 12288 x 3072):
 //  * v_mfma_f32_16x16x32_bf16 sustains 1.68 PF/s (one wave per SIMD) and
@@ -44,15 +44,18 @@
 //      4096w + 2048g + 512j + 32c + 16(h ^ (c >> 3)) -- each DMA moves 32 whole
 //      32-byte column segments, and the 16 columns of one operand read (fixed
 //      g, j, h) fill the 16 16-byte bank slots
-//   S  [K/2,N]: [2 K groups][256 B] E8M0 scales of the stage's columns
+//      G: the tile's two 128-column blocks as stored, [block][8 chunks of 8 K]
+//      [128 columns][4 B] (each DMA is 1 KB of contiguous HBM); the words of
+//      columns 4c .. 4c+3 are one 16-byte read
+//   S  [K/2,N] and G: [2 K groups][256 B] E8M0 scales of the stage's columns
 //      [N,K/2]: [256 columns][4 B]: the column's scale dword of the stage pair
 //      (K groups 4u .. 4u+3 for stages 2u, 2u+1); a stage uses bytes
 //      2 (stage % 2) + 0, 1
 // MFMA v_mfma_f32_16x16x32_bf16: lane l holds A row l % 16, K 8(l / 16) .. +7
 // of the 32-K sub-step, and B column 4c + j of a 64-column group (c = l % 16,
 // MFMA j of the group): [K/2,N] byte j of the four K-pair rows 4(l / 16) ..
-// +3, [N,K/2] word l / 16 of the column's half; the result holds rows
-// 4(l / 16) .. +3 of that column.
+// +3, [N,K/2] word l / 16 of the column's half, G the column's word of chunk
+// 4 sub + l / 16; the result holds rows 4(l / 16) .. +3 of that column.
 //
 // Reference counterpart: the K loop of strategy_j / strategy_m
 // (csrc/strategy_j_synthesis.cu:120-170, csrc/strategy_m_asm.cu:131-185).
@@ -76,14 +79,14 @@ constexpr int kBDma = kBBytes / 1024 / kWaves;  // 2
 constexpr int kVmPerStage = kADma + kBDma + 1;  // + one scale DMA
 static_assert(2 * kVmPerStage < 64, "vmcnt range");
 
-// Per-layout LDS sizes: [K/2,N] stages hold 2 x 256 scale bytes (two of the
-// four waves move them; the other two DMA into a spare 256-byte window),
-// [N,K/2] stages 256 scale dwords (one DMA per wave).
+// Per-layout LDS sizes: [K/2,N] and G stages hold 2 x 256 scale bytes (two
+// of the four waves move them; the other two DMA into a spare 256-byte
+// window), [N,K/2] stages 256 scale dwords (one DMA per wave).
 template <int L>
 struct SchedLds {
-  static constexpr int kSBytes = L == kLayoutKN ? 2 * kBN : 4 * kBN;
+  static constexpr int kSBytes = L == kLayoutNK ? 4 * kBN : 2 * kBN;
   static constexpr int kStage = kABytes + kBBytes + kSBytes;
-  static constexpr int kLds = kNS * kStage + (L == kLayoutKN ? 256 : 0);
+  static constexpr int kLds = kNS * kStage + (L == kLayoutNK ? 0 : 256);
   static_assert(kStage % 256 == 0, "slot offsets are ds_read2st64 immediates");
   static_assert(2 * kLds <= 160 * 1024, "two CTAs per CU");
 };
@@ -160,8 +163,9 @@ __device__ __forceinline__ float e8m0_byte(uint32_t w, int j) {
 // stores went through scratch.
 template <int L, int kOut>
 __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
-  static_assert(L == kLayoutKN || L == kLayoutNK, "plain layouts");
-  constexpr bool kKN = L == kLayoutKN;
+  static_assert(L == kLayoutKN || L == kLayoutNK || L == kLayoutG, "layout");
+  constexpr bool kKN = L == kLayoutKN, kG = L == kLayoutG;
+  constexpr bool kScRows = !(L == kLayoutNK);  // scales in LDS as [2 K groups][256 columns]
   constexpr int kStage = SchedLds<L>::kStage;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SchedLds<L>::kLds];
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
@@ -191,6 +195,8 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
   // ---- loop-invariant DMA offsets (the K step goes in soffset) ---------------
   const desc_t dA = make_desc(p.A + (size_t)m0 * K);
   const int G = K / 32;
+  // G: the tile's two 128-column blocks start at byte n0 * K/2 (codes) and
+  // n0 * K/32 (scales), like [N,K/2]
   const desc_t dB = make_desc(kKN ? p.B + n0 : p.B + (size_t)n0 * (K / 2));
   const desc_t dS = make_desc(kKN ? p.S + n0 : p.S + (size_t)n0 * G);
   const desc_t dNull = make_desc(p.A, 0u);  // every lane out of range: writes zeros
@@ -212,6 +218,11 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
       const int row = qq >> 4;
       const int lc = (qq & 15) ^ (4 * ((row >> 2) & 3));
       vb[ii] = n0 + lc * 16 < N ? (uint32_t)(row * N + lc * 16) : kOobOffset;
+    } else if constexpr (kG) {
+      // DMA d covers 8-K chunks 2(d % 4), +1 of block d / 4: 1 KB contiguous,
+      // landing as [block][8 chunks][128 columns][4 B]
+      const int blk = d >> 2;
+      vb[ii] = n0 + 128 * blk < N ? (uint32_t)((blk * (K / 8) + 2 * (d & 3)) * 512 + 16 * lane) : kOobOffset;
     } else {
       // DMA d = 4w + 2g + j/2 covers columns 128w + 64g + 4c + j (c = 0..15,
       // j = 2 (d % 2) + cl / 16) of lane pair cl = lane / 2; lane bit h' is
@@ -226,12 +237,18 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
   // columns each); waves 2, 3 issue the same DMA into a spare window so every
   // wave counts the same number of loads per stage.  [N,K/2]: wave w moves
   // the stage pair's dword of columns 64w .. 64w+63.
-  const bool sc_wave = !kKN || wave < 2;
+  // G: wave kg < 2 moves K group kg of both blocks (lane / 32 = block), into
+  // the [K/2,N] arrangement.
+  const bool sc_wave = !kScRows || wave < 2;
   uint32_t vs;
-  if constexpr (kKN)
+  if constexpr (kKN) {
     vs = sc_wave && n0 + 4 * lane < N ? (uint32_t)(wave * N + 4 * lane) : kOobOffset;
-  else
+  } else if constexpr (kG) {
+    const int blk = lane >> 5;
+    vs = sc_wave && n0 + 128 * blk < N ? (uint32_t)((blk * G + wave) * 128 + 4 * (lane & 31)) : kOobOffset;
+  } else {
     vs = n0 + 64 * wave + lane < N ? (uint32_t)((64 * wave + lane) * G) : kOobOffset;
+  }
   const uint32_t sc_lds = sc_wave ? (uint32_t)(kABytes + kBBytes + 256 * wave) : 0u;
 
   auto issue_a = [&](int ii, int slot, int step, bool live) __attribute__((always_inline)) {
@@ -240,11 +257,13 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
   };
   auto issue_b = [&](int ii, int slot, int step, bool live) __attribute__((always_inline)) {
     dma16s(live ? dB : dNull, lds0 + slot * kStage + kABytes + (wave * kBDma + ii) * 1024, vb[ii],
-           kKN ? (uint32_t)step * (kBK / 2) * (uint32_t)N : (uint32_t)step * (kBK / 2));
+           kKN ? (uint32_t)step * (kBK / 2) * (uint32_t)N
+               : kG ? (uint32_t)step * 4096u : (uint32_t)step * (kBK / 2));
   };
   auto issue_s = [&](int slot, int step, bool live) __attribute__((always_inline)) {
     dma4s(live ? dS : dNull, sc_wave ? lds0 + slot * kStage + sc_lds : lds0 + kNS * kStage, vs,
-          kKN ? (uint32_t)step * 2u * (uint32_t)N : (uint32_t)(step >> 1) * 4u);
+          kKN ? (uint32_t)step * 2u * (uint32_t)N
+              : kG ? (uint32_t)step * 256u : (uint32_t)(step >> 1) * 4u);
   };
   // DMA number d (0 .. kVmPerStage-1) of a stage
   auto issue_dma = [&](int d, int slot, int step, bool live) __attribute__((always_inline)) {
@@ -272,15 +291,18 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
     if constexpr (kKN) {
       const int colb = wn * 128 + 64 * i + 4 * c;
       b_off[i] = lds0 + (uint32_t)(kABytes + 4 * q * kBN + (((colb >> 4) ^ (4 * q)) * 16) + (colb & 15));
+    } else if constexpr (kG) {
+      // chunk 4 sub + q of block wn, columns 4c .. 4c+3 (+ 64 g: immediate)
+      b_off[i] = lds0 + (uint32_t)(kABytes + 4096 * wn + 512 * (4 * i + q) + 16 * c);
     } else {
       b_off[i] = lds0 + (uint32_t)(kABytes + 4096 * wn + 32 * c + 16 * (i ^ (c >> 3)) + 4 * q);
     }
   }
   // scales: [K/2,N] bytes of columns wn*128 + 4c .. +3 (+ 64 g), [N,K/2] their
   // dwords
-  const uint32_t s_off = kKN ? lds0 + (uint32_t)(kABytes + kBBytes + wn * 128 + 4 * c)
-                             : lds0 + (uint32_t)(kABytes + kBBytes + wn * 512 + 16 * c);
-  using ScaleWords = std::conditional_t<kKN, u32x2, u32x4>;
+  const uint32_t s_off = kScRows ? lds0 + (uint32_t)(kABytes + kBBytes + wn * 128 + 4 * c)
+                                 : lds0 + (uint32_t)(kABytes + kBBytes + wn * 512 + 16 * c);
+  using ScaleWords = std::conditional_t<kScRows, u32x2, u32x4>;
 
   f32x4 acc[kRB][kCB];
 #pragma unroll
@@ -303,7 +325,15 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
         u32x2 x, y;
-        if constexpr (kKN) {
+        if constexpr (kG) {
+          // the words of columns 4c + j, j = 0..3, are 16 contiguous bytes
+          const u32x4 v = __builtin_bit_cast(u32x4, g == 0 ? (sub == 0 ? lds_b128<O * 256>(b_off[0])
+                                                                       : lds_b128<O * 256>(b_off[1]))
+                                                           : (sub == 0 ? lds_b128<O * 256 + 256>(b_off[0])
+                                                                       : lds_b128<O * 256 + 256>(b_off[1])));
+          r[4 * g + 0] = v.x; r[4 * g + 1] = v.y; r[4 * g + 2] = v.z; r[4 * g + 3] = v.w;
+          continue;
+        } else if constexpr (kKN) {
           if (sub == 0) {
             x = lds_2st64<O + 0, O + 1>(b_off[g]);
             y = lds_2st64<O + 2, O + 3>(b_off[g]);
@@ -336,7 +366,7 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
     // scale words of column group 0 (w) and 1 (x): [K/2,N] K group 0, 1;
     // [N,K/2] the dwords of columns 4c + j
     auto read_scales = [&](auto slot_c, ScaleWords& w, ScaleWords& x) __attribute__((always_inline)) {
-      if constexpr (kKN) {
+      if constexpr (kScRows) {
         constexpr int O = decltype(slot_c)::value * (kStage / 256);
         w = lds_2st64<O, O + 1>(s_off);
         x = lds_2st64<O, O + 1>(s_off + 64);
@@ -349,7 +379,7 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
     // step: the absolute K step of the scales ([N,K/2]: its parity picks the
     // half of the stage pair's dword)
     auto scales_from = [&](ScaleWords w, ScaleWords x, int step) __attribute__((always_inline)) {
-      if constexpr (kKN) {
+      if constexpr (kScRows) {
         (void)step;
 #pragma unroll
         for (int kg = 0; kg < 2; ++kg)
@@ -538,7 +568,7 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
 }  // namespace
 
 bool tiled_sched_available(int layout, const TiledShape& s) {
-  return (layout == kLayoutKN || layout == kLayoutNK) && s.bm() == kBM && s.bn() == kBN &&
+  return (layout == kLayoutKN || layout == kLayoutNK || layout == kLayoutG) && s.bm() == kBM && s.bn() == kBN &&
          s.wm * s.wn == kWaves && s.stages == kNS;
 }
 
@@ -559,8 +589,10 @@ hipError_t launch_tiled_sched(int layout, const TiledShape& shape, const TiledAr
   const int grid = args.tiles_m * args.tiles_n * args.splits;
   if (layout == kLayoutKN)
     launch_sched_layout<kLayoutKN>(args, grid, stream);
-  else
+  else if (layout == kLayoutNK)
     launch_sched_layout<kLayoutNK>(args, grid, stream);
+  else
+    launch_sched_layout<kLayoutG>(args, grid, stream);
   return hipGetLastError();
 }
 

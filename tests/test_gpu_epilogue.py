@@ -79,7 +79,7 @@ def check(kk, M, N, K, layout, plan, seed=0):
 @pytest.mark.parametrize("layout,plan", [
     ("kn", (2, 6, 1)), ("kn", (2, 6, 3)), ("nk", (2, 10, 2)), ("g", (2, 6, 1)), ("p", (2, 10, 3)),
     ("kn", (2, 1, 1)), ("nk", (2, 0, 2)), ("kn", (2, 15, 1)), ("kn", (2, 15, 3)),
-    ("nk", (2, 15, 1)), ("nk", (2, 15, 3)),
+    ("nk", (2, 15, 1)), ("nk", (2, 15, 3)), ("g", (2, 15, 1)), ("g", (2, 15, 3)),
 ])
 def test_epilogue_tiled(kk, layout, plan):
     check(kk, 300, 512, 640, layout, plan)

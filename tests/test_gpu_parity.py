@@ -123,7 +123,7 @@ def test_generic_kernel_odd_n(kk):
 
 TILED_VARIANTS = range(16)
 PIPE_VARIANTS = range(6, 15)  # pipelined kernel; [N,K/2] needs K % 128 == 0
-SCHED_VARIANT = 15            # hand-scheduled kernel: [K/2,N] with K % 64 == 0, [N,K/2] with K % 128 == 0
+SCHED_VARIANT = 15            # hand-scheduled kernel: [K/2,N] and G with K % 64 == 0, [N,K/2] with K % 128 == 0
 GEMV_VARIANTS = range(15)
 
 
@@ -148,7 +148,7 @@ def test_every_tiled_variant_and_split(kk, layout, K):
             assert bad == 0, f"variant {v} split {split}: {bad} bad"
 
 
-@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("layout", ["kn", "nk", "g"])
 @pytest.mark.parametrize("M,N,K", [(300, 528, 640), (64, 256, 128), (513, 1040, 1536)])
 def test_sched_kernel_tails_and_splits(kk, layout, M, N, K):
     """Hand-scheduled kernel: M / N tails (N % 256 != 0), splits down to one
@@ -158,6 +158,8 @@ def test_sched_kernel_tails_and_splits(kk, layout, M, N, K):
     and bf16 out is the fp32 result rounded."""
     import torch
 
+    if layout == "g":
+        N = -(-N // 128) * 128  # G blocks are 128 columns; 640 / 1152 leave a half-empty last tile
     A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=33)
     ref = oracle_f64(A_bits, W, S)
     plan = lambda split: (kk.KERNEL_TILED, SCHED_VARIANT, split)

@@ -162,7 +162,7 @@ def test_layout_shape_rules(lib):
     (16, 8192, 8192, mo.LAYOUT_P, 4, "stream"),
     (32, 8192, 8192, mo.LAYOUT_P, 4, "stream"),
     (16, 8192, 8192, mo.LAYOUT_G, 2, "tiled-pipe"),
-    (4096, 12288, 3072, mo.LAYOUT_G, 2, "tiled-pipe"),
+    (4096, 12288, 3072, mo.LAYOUT_G, 2, "tiled-sched"),
     (4096, 12288, 3072, mo.LAYOUT_P, 2, "tiled-pipe"),
     (64, 96, 64, mo.LAYOUT_P, 2, "tiled-pipe"),
 ])
@@ -170,7 +170,7 @@ def test_prepacked_layouts_plan_native_kernels(lib, M, N, K, layout, kernel, pre
     rc, p, desc = _plan(lib, M, N, K, layout)
     assert rc == hipSuccess
     assert p.kernel == kernel and desc.startswith(prefix), desc
-    # a non-pipelined tiled variant has no G / P loader: rejected
+    # the first tiled kernel has no G / P loader: rejected
     assert lib.mxfp4_gemm_workspace_bytes(M, N, K, layout, ctypes.byref(Plan(2, 1, 2, 0))) == 0
     # the GEMV family has none either
     assert lib.mxfp4_gemm_workspace_bytes(M, N, K, layout, ctypes.byref(Plan(1, 0, 2, 0))) == 0
