@@ -160,7 +160,11 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
   }
   int want;
   if (layout == kLayoutKN)
-    want = two ? 4 : 0;  // (2,8,8,2) / (1,8,8,4)
+    // (2,8,8,2) / (1,8,8,4); M <= 16 with N >= 24576: 256-column CTAs and
+    // split 2 (N = 28672, K = 8192: 28.5 / 29.9 / 32.2 us at M = 1 / 8 / 16
+    // against 29.8 / 32.4 / 35.8 us with 128-column CTAs, which at N = 8192
+    // are the faster ones)
+    want = two ? 4 : N >= 24576 ? 1 : 0;
   else
     want = two ? 7 : 6;  // (2,2,16,2) / (1,2,16,4)
   const GemvShape& g = kGemv[want];
