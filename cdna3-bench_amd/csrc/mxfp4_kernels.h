@@ -92,10 +92,11 @@ hipError_t launch_gemv(int layout, const GemvShape& shape, const GemvArgs& args,
                        hipStream_t stream);
 bool gemv_shape_available(int layout, const GemvShape& shape);
 
-// Streaming split-K family for M <= 32 and [N,K/2] or P weights (mxfp4_stream.hip):
-// 32-column groups, K in `splits` ranges of waves * kw, one CTA per
-// (group block, split) processing `splits` units; partials travel as tagged
-// packets.
+// Streaming family for M <= 32 and [N,K/2] or P weights (mxfp4_stream.hip).
+// Split-K kernel: 32-column groups, K in `splits` ranges of waves * kw, one
+// CTA per (group block, split) processing `splits` units; partials travel as
+// tagged packets.  Whole-K kernel (nslot == 1, splits == 1): one CTA of
+// K / kw waves per 32-column group.
 struct StreamArgs {
   const uint16_t* A;
   const uint8_t* B;
@@ -104,7 +105,7 @@ struct StreamArgs {
   int M, N, K;
   int out_bf16;
   int splits;           // ceil(K / (waves * 256)), <= smax
-  int groups;           // ceil(N / 32)
+  int groups;           // ceil(N / 32): 32-column groups
   int ctas;             // ceil(groups / splits) * splits
   float* partials;      // splits > 1: [ctas][splits][16*mt*32] packets of 8 bytes, zero on entry/exit
   uint32_t* counters;   // splits > 1: [ctas], zero on entry, zero on exit

@@ -114,7 +114,8 @@ class StrategyDesc:
 
 
 # Measured on MI355X with seeded random data (A ~ N(0,1), uniform codes):
-#  * tiled-sched: dit_up 0.54, 70B FFN M=2048..8192 0.58 (plan variant 15);
+#  * tiled-sched: dit_up 0.55 ([K/2,N]), 0.57 (G), 0.49 ([N,K/2]), 70B FFN
+#    M=2048..8192 0.58 (plan variant 15);
 #  * tiled-pipe: dit_up 0.52 ([K/2,N]), 0.40 ([N,K/2]) (plan variant 6);
 #  * stream: decode M=16 N=K=8192 [N,K/2] 2.69 TB/s, P layout 3.03 TB/s;
 #  * stream-whole: M=1 N=K=8192 [N,K/2] 3.37 TB/s (P 3.59), N=28672 3.87 TB/s;

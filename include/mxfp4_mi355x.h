@@ -55,7 +55,8 @@ enum {
   MXFP4_KERNEL_GEMV = 1,    /* memory-bound family, M <= 32 */
   MXFP4_KERNEL_TILED = 2,   /* MFMA-bound tiled family */
   MXFP4_KERNEL_GENERIC = 3, /* one thread per output, any N */
-  MXFP4_KERNEL_STREAM = 4   /* split-K weight streaming, M <= 32, NK or P layout, K % 256 == 0 */
+  MXFP4_KERNEL_STREAM = 4   /* weight streaming, M <= 32, NK or P layout, K % 256 == 0: split-K
+                               (variants 0-4) and whole-K (5, 6: M <= 16) kernels */
 };
 
 /* A launch plan: which kernel family, which tile variant, how many K splits. */
