@@ -41,24 +41,29 @@ struct TiledVariant {
 // uniform E2M1 codes), where power limits the MFMA rate well below peak.
 // Variants 6 and 15 were re-measured after the store-loop change (dit_up,
 // dit_down and the 70B FFN shapes at M = 512 .. 8192: variant 15 reaches
-// 0.53-0.58, variant 6 0.52-0.56 of 2.5 PF/s); the others predate it and are
-// conservative.
+// 0.53-0.58, variant 6 0.52-0.56 of 2.5 PF/s); 3 and 5 after the split-K
+// reduction change at M = 48 .. 1024 (where 7 and 15 measure alike).  The
+// model then picks within ~5 % of the best measured plan on those shapes,
+// except M = 64, N = K = 8192 (variant 5 split 4: 44 us, split 8: 33 us).
 const TiledVariant kTiled[] = {
-    {{2, 2, 4}, 0.35, 0.31, 1, kFamilyPlain},       // 0: 256 x 256, 4 waves, 128 x 128 per wave
-    {{4, 2, 2}, 0.42, 0.33, 1, kFamilyPlain},       // 1: 256 x 256, 8 waves
-    {{2, 2, 2}, 0.28, 0.23, 2, kFamilyPlain},       // 2: 128 x 256
-    {{1, 2, 2}, 0.30, 0.26, 2, kFamilyPlain},       // 3:  64 x 256
-    {{2, 1, 2}, 0.26, 0.27, 2, kFamilyPlain},       // 4: 128 x 128
-    {{1, 2, 1}, 0.20, 0.17, 4, kFamilyPlain},       // 5:  32 x 256
+    // 0, 1, 2, 4, 8 .. 14: explicit plans only (efficiency 0: never
+    // auto-selected); their last calibration predates the store-loop and
+    // split-K changes
+    {{2, 2, 4}, 0.0, 0.0, 1, kFamilyPlain},         // 0: 256 x 256, 4 waves, 128 x 128 per wave
+    {{4, 2, 2}, 0.0, 0.0, 1, kFamilyPlain},         // 1: 256 x 256, 8 waves
+    {{2, 2, 2}, 0.0, 0.0, 2, kFamilyPlain},         // 2: 128 x 256
+    {{1, 2, 2}, 0.17, 0.15, 2, kFamilyPlain},       // 3:  64 x 256 (re-measured at M = 64 .. 256)
+    {{2, 1, 2}, 0.0, 0.0, 2, kFamilyPlain},         // 4: 128 x 128
+    {{1, 2, 1}, 0.15, 0.13, 4, kFamilyPlain},       // 5:  32 x 256 (re-measured at M = 48 .. 1024)
     {{4, 2, 2, 4, 3}, 0.52, 0.40, 1, kFamilyPipe}, // 6: pipelined 256 x 256, 8 waves of 64 x 128, 3 stages
     {{2, 2, 2, 4, 3}, 0.32, 0.23, 1, kFamilyPipe},  // 7: pipelined 128 x 256, 4 waves of 64 x 128
-    {{4, 2, 2, 4, 3}, 0.432, 0.333, 1, kFamilyPipe},// 8: = 6 (a 4-stage 256 x 256 ring no longer fits 160 KB)
-    {{2, 4, 4, 2, 3}, 0.37, 0.361, 1, kFamilyPipe}, // 9: = 10
-    {{2, 4, 4, 2, 3}, 0.37, 0.361, 1, kFamilyPipe}, // 10: as 9 with 3 stages
-    {{2, 2, 2, 4, 4}, 0.33, 0.23, 1, kFamilyPipe},  // 11: as 7 with 4 stages
-    {{2, 4, 2, 2, 4}, 0.31, 0.26, 1, kFamilyPipe},  // 12: pipelined 128 x 256, 8 waves of 64 x 64
-    {{1, 4, 4, 2, 4}, 0.32, 0.25, 1, kFamilyPipe},  // 13: pipelined 128 x 256, 4 waves of 128 x 64
-    {{2, 1, 2, 4, 4}, 0.28, 0.24, 2, kFamilyPipe},  // 14: pipelined 128 x 128, 2 waves
+    {{4, 2, 2, 4, 3}, 0.0, 0.0, 1, kFamilyPipe},   // 8: = 6 (a 4-stage 256 x 256 ring no longer fits 160 KB)
+    {{2, 4, 4, 2, 3}, 0.0, 0.0, 1, kFamilyPipe},   // 9: = 10
+    {{2, 4, 4, 2, 3}, 0.0, 0.0, 1, kFamilyPipe},   // 10: pipelined 256 x 256, 8 waves of 128 x 64, 3 stages
+    {{2, 2, 2, 4, 4}, 0.0, 0.0, 1, kFamilyPipe},   // 11: as 7 with 4 stages
+    {{2, 4, 2, 2, 4}, 0.0, 0.0, 1, kFamilyPipe},   // 12: pipelined 128 x 256, 8 waves of 64 x 64
+    {{1, 4, 4, 2, 4}, 0.0, 0.0, 1, kFamilyPipe},   // 13: pipelined 128 x 256, 4 waves of 128 x 64
+    {{2, 1, 2, 4, 4}, 0.0, 0.0, 2, kFamilyPipe},   // 14: pipelined 128 x 128, 2 waves
     {{2, 2, 2, 4, 3}, 0.55, 0.52, 2, kFamilySched}, // 15: hand-scheduled 128 x 256, 4 waves of 64 x 128, 2 CTAs / CU
 };
 constexpr int kNumTiled = sizeof(kTiled) / sizeof(kTiled[0]);
@@ -205,14 +210,22 @@ double tiled_time(const TiledVariant& v, int layout, int64_t M, int64_t N, int64
   const int64_t ctas = tiles * ceil_div(ksteps, per_split);
   const double slots = kNumCus * v.ctas_per_cu;
   const double rounds = std::ceil((double)ctas / slots);
-  const double cu_rate = kMfmaFlopsPerS / kNumCus * tiled_eff(v, layout);
-  const double t_cta = (double)bm * bn * per_split * 64 * 2.0 * v.ctas_per_cu / cu_rate;
+  // CTAs per CU in a round: a variant calibrated at two CTAs per CU runs a
+  // lone CTA at one wave per SIMD, ~0.88 of the CU's two-wave MFMA rate
+  // (1.68 vs 1.91 PF/s on random operands)
+  const double share = std::min<double>(v.ctas_per_cu, std::ceil((double)ctas / (rounds * kNumCus)));
+  const double solo = v.ctas_per_cu > 1 && share < 2 ? 0.88 : 1.0;
+  const double cu_rate = kMfmaFlopsPerS / kNumCus * tiled_eff(v, layout) * solo;
+  const double t_cta = (double)bm * bn * per_split * 64 * 2.0 * share / cu_rate;
   double t = rounds * t_cta;
   const double t_hbm = problem_bytes(M, N, K, 2) / kHbmBytesPerS;
   t = std::max(t, t_hbm);
   // split-K: partial traffic plus the last CTA's serial tail (coherent store,
-  // counter, coherent loads: ~3 memory round trips).
-  if (splits > 1) t += 2.0 * tiles * splits * (double)bm * bn * 4.0 / kHbmBytesPerS + 3.0e-6;
+  // counter, then coherent loads of every split's partial tile at roughly one
+  // CU's bandwidth, ~100 GB/s; measured on the 70B FFN at M = 128: split 2
+  // 81 us, split 4 92 us).
+  if (splits > 1)
+    t += 2.0 * tiles * splits * (double)bm * bn * 4.0 / kHbmBytesPerS + 1.5e-6 + splits * (double)bm * bn * 4.0 / 1.0e11;
   return t + kLaunchS;
 }
 
@@ -222,7 +235,7 @@ void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) 
   const int64_t ksteps = ceil_div(K, 64);
   for (int v = 0; v < kNumTiled; ++v) {
     const TiledVariant& tv = kTiled[v];
-    if (!tiled_variant_ok(tv, layout, K)) continue;
+    if (!tiled_variant_ok(tv, layout, K) || tiled_eff(tv, layout) <= 0.0) continue;
     const int64_t tiles = ceil_div(M, tv.shape.bm()) * ceil_div(N, tv.shape.bn());
     for (int s = 1; s <= 16 && s <= ksteps; ++s) {
       if (s > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) break;

@@ -186,6 +186,33 @@ __device__ __forceinline__ bool splitk_arrive_last(uint32_t* counter, uint32_t s
   return *s_flag != 0;
 }
 
+// The last CTA's sum of a tile's split partials: Q f32x4 per thread, element
+// i of split sp at byte sp * slot + (i * nt + threadIdx.x) * 16.  Each
+// element's splits are added in split order (bit-reproducible).  The loads go
+// GRP elements at a time, one split's GRP loads in flight together: S * Q /
+// GRP memory round trips (an element-by-element loop waited for every load,
+// S * Q round trips -- 160 us of tail at S = 16).  put(i, sum) stores the
+// result.
+template <int Q, int GRP = 8, typename Put>
+__device__ __forceinline__ void splitk_sum(__amdgpu_buffer_rsrc_t rp, uint32_t slot, int splits, uint32_t nt,
+                                           Put&& put) {
+  static_assert(Q % GRP == 0, "whole groups");
+#pragma unroll
+  for (int g0 = 0; g0 < Q; g0 += GRP) {
+    f32x4 sum[GRP];
+    for (int sp = 0; sp < splits; ++sp) {
+      f32x4 t[GRP];
+#pragma unroll
+      for (int b = 0; b < GRP; ++b)
+        t[b] = load_coherent4(rp, sp * slot + (uint32_t)((g0 + b) * nt + threadIdx.x) * 16);
+#pragma unroll
+      for (int b = 0; b < GRP; ++b) sum[b] = sp == 0 ? t[b] : sum[b] + t[b];
+    }
+#pragma unroll
+    for (int b = 0; b < GRP; ++b) put(g0 + b, sum[b]);
+  }
+}
+
 // Workgroups are dispatched round-robin over the XCDs (id % 8).  Renumber so
 // each XCD owns one contiguous range of logical ids; a bijection for any
 // count.  Neighbouring logical tiles then share an XCD's L2.

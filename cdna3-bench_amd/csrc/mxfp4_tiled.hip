@@ -266,18 +266,11 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_kernel(TiledArgs p) {
           store_coherent(rp, off, v);
         }
     if (!splitk_arrive_last(p.counters + tile, (uint32_t)p.splits, &s_last)) return;
+    splitk_sum<RB * 16>(rp, SLOT, p.splits, NT, [&](int i, f32x4 v) __attribute__((always_inline)) {
+      const int rb = i / 16, j = (i / 4) % 4, q4 = i % 4;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const uint32_t off = (uint32_t)(((rb * 4 + j) * 4 + q4) * NT + threadIdx.x) * 16;
-          f32x4 sum = load_coherent4(rp, off);
-          for (int sp = 1; sp < p.splits; ++sp) sum += load_coherent4(rp, sp * SLOT + off);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[rb][j][q4 * 4 + e] = sum[e];
-        }
+      for (int e = 0; e < 4; ++e) acc[rb][j][q4 * 4 + e] = v[e];
+    });
   }
 
   // ---- epilogue ------------------------------------------------------------

@@ -449,18 +449,11 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
           store_coherent(rp, split * SLOT + (uint32_t)(((rb * WNC + j) * 4 + q4) * NT + threadIdx.x) * 16, v);
         }
     if (!splitk_arrive_last(p.counters + tile, (uint32_t)p.splits, s_last)) return;
+    splitk_sum<RB * WNC * 4>(rp, SLOT, p.splits, NT, [&](int i, f32x4 v) __attribute__((always_inline)) {
+      const int rb = i / (WNC * 4), j = (i / 4) % WNC, q4 = i % 4;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int j = 0; j < WNC; ++j)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const uint32_t off = (uint32_t)(((rb * WNC + j) * 4 + q4) * NT + threadIdx.x) * 16;
-          f32x4 sum = load_coherent4(rp, off);
-          for (int sp = 1; sp < p.splits; ++sp) sum += load_coherent4(rp, sp * SLOT + off);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[rb][j][q4 * 4 + e] = sum[e];
-        }
+      for (int e = 0; e < 4; ++e) acc[rb][j][q4 * 4 + e] = v[e];
+    });
   }
 
   // ---- epilogue ----------------------------------------------------------------

@@ -519,15 +519,8 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
       for (int cb = 0; cb < kCB; ++cb)
         store_coherent(rp, split * SLOT + (uint32_t)((rb * kCB + cb) * kThreads + threadIdx.x) * 16, acc[rb][cb]);
     if (!splitk_arrive_last(p.counters + tile, (uint32_t)p.splits, s_last)) return;
-#pragma unroll
-    for (int rb = 0; rb < kRB; ++rb)
-#pragma unroll
-      for (int cb = 0; cb < kCB; ++cb) {
-        const uint32_t off = (uint32_t)((rb * kCB + cb) * kThreads + threadIdx.x) * 16;
-        f32x4 sum = load_coherent4(rp, off);
-        for (int sp = 1; sp < p.splits; ++sp) sum += load_coherent4(rp, sp * SLOT + off);
-        acc[rb][cb] = sum;
-      }
+    splitk_sum<Q>(rp, SLOT, p.splits, kThreads,
+                  [&](int i, f32x4 v) __attribute__((always_inline)) { acc[i / kCB][i % kCB] = v; });
   }
 
   // ---- epilogue: 4 adjacent columns (blocks 4g .. 4g+3) per lane and row --------

