@@ -227,16 +227,22 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
         if (live(e) && row_of(e) < M)
           store_coherent(rp, (uint32_t)((split * TILE + row_of(e) * COLS + col_of(ch, e)) * 4), v[ch][e]);
     if (!splitk_arrive_last(p.counters + cg, (uint32_t)p.splits, &s_last)) return;
+    // the splits in split order, every element of one split in flight at once
+    // (a per-element loop waited for each load: splits x elements round trips)
+    for (int sp = 0; sp < p.splits; ++sp) {
+      float t[CHUNKS][PER];
 #pragma unroll
-    for (int ch = 0; ch < CHUNKS; ++ch)
+      for (int ch = 0; ch < CHUNKS; ++ch)
 #pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        if (!live(e) || row_of(e) >= M) continue;
-        const uint32_t off = (uint32_t)((row_of(e) * COLS + col_of(ch, e)) * 4);
-        float sum = load_coherent1(rp, off);
-        for (int sp = 1; sp < p.splits; ++sp) sum += load_coherent1(rp, off + (uint32_t)(sp * TILE * 4));
-        v[ch][e] = sum;
-      }
+        for (int e = 0; e < PER; ++e)
+          t[ch][e] = live(e) && row_of(e) < M
+                         ? load_coherent1(rp, (uint32_t)((sp * TILE + row_of(e) * COLS + col_of(ch, e)) * 4))
+                         : 0.f;
+#pragma unroll
+      for (int ch = 0; ch < CHUNKS; ++ch)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) v[ch][e] = sp == 0 ? t[ch][e] : v[ch][e] + t[ch][e];
+    }
   }
 
   // plain and fused stores are separate loops, chosen once (see StoreKind)
