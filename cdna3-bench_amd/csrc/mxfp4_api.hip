@@ -43,8 +43,7 @@ struct TiledVariant {
 // dit_down and the 70B FFN shapes at M = 512 .. 8192: variant 15 reaches
 // 0.53-0.58, variant 6 0.52-0.56 of 2.5 PF/s); 3 and 5 after the split-K
 // reduction change at M = 48 .. 1024 (where 7 and 15 measure alike).  The
-// model then picks within ~5 % of the best measured plan on those shapes,
-// except M = 64, N = K = 8192 (variant 5 split 4: 44 us, split 8: 33 us).
+// model then picks within 10 % of the best measured plan on those shapes.
 const TiledVariant kTiled[] = {
     // 0, 1, 2, 4, 8 .. 14: explicit plans only (efficiency 0: never
     // auto-selected); their last calibration predates the store-loop and
@@ -210,12 +209,16 @@ double tiled_time(const TiledVariant& v, int layout, int64_t M, int64_t N, int64
   const int64_t ctas = tiles * ceil_div(ksteps, per_split);
   const double slots = kNumCus * v.ctas_per_cu;
   const double rounds = std::ceil((double)ctas / slots);
-  // CTAs per CU in a round: a variant calibrated at two CTAs per CU runs a
-  // lone CTA at one wave per SIMD, ~0.88 of the CU's two-wave MFMA rate
-  // (1.68 vs 1.91 PF/s on random operands)
+  // CTAs per CU in a round, and the CU's MFMA rate at that residency
+  // relative to the one the efficiency was calibrated at: SIMDs without a
+  // wave idle, and a SIMD with one wave runs at ~0.88 of two (1.68 vs 1.91
+  // PF/s on random operands)
   const double share = std::min<double>(v.ctas_per_cu, std::ceil((double)ctas / (rounds * kNumCus)));
-  const double solo = v.ctas_per_cu > 1 && share < 2 ? 0.88 : 1.0;
-  const double cu_rate = kMfmaFlopsPerS / kNumCus * tiled_eff(v, layout) * solo;
+  auto fill = [&](double ctas_on_cu) {
+    const double per_simd = ctas_on_cu * v.shape.wm * v.shape.wn / 4.0;
+    return std::min(1.0, per_simd) * (per_simd >= 2.0 ? 1.0 : 0.88);
+  };
+  const double cu_rate = kMfmaFlopsPerS / kNumCus * tiled_eff(v, layout) * fill(share) / fill(v.ctas_per_cu);
   const double t_cta = (double)bm * bn * per_split * 64 * 2.0 * share / cu_rate;
   double t = rounds * t_cta;
   const double t_hbm = problem_bytes(M, N, K, 2) / kHbmBytesPerS;
