@@ -43,7 +43,7 @@ struct TiledVariant {
 // dit_down and the 70B FFN shapes at M = 512 .. 8192: variant 15 reaches
 // 0.53-0.58, variant 6 0.52-0.56 of 2.5 PF/s); 3 and 5 after the split-K
 // reduction change at M = 48 .. 1024 (where 7 and 15 measure alike).  The
-// model then picks within 10 % of the best measured plan on those shapes.
+// model then picks within 12 % of the best measured plan on those shapes.
 const TiledVariant kTiled[] = {
     // 0, 1, 2, 4, 8 .. 14: explicit plans only (efficiency 0: never
     // auto-selected); their last calibration predates the store-loop and

@@ -199,3 +199,29 @@ def test_product_package_never_imports_oracle():
             if f.endswith((".py", ".cpp", ".hip", ".h")):
                 text = open(os.path.join(root, f)).read()
                 assert "oracle" not in re.sub(r"#.*|//.*", "", text).replace("oracle/", ""), f
+
+
+# Measured on MI355X ([K/2,N], bench.py's method: graph-replayed, seeded
+# random data): microseconds per call of tiled plans (variant, split) on small
+# and medium shapes.  The selector's pick must be within 12 % of the best of
+# these (the cost model's residency and split-tail terms were fitted to them).
+MEASURED_TILED_US = {
+    (48, 4096, 4096): {(5, 8): 19.9, (5, 4): 23.8, (15, 4): 27.1, (7, 4): 26.9, (3, 8): 28.7, (5, 13): 22.3},
+    (64, 8192, 8192): {(5, 8): 33.2, (5, 4): 43.9, (15, 8): 39.3, (7, 8): 40.2, (3, 8): 42.2},
+    (128, 8192, 8192): {(15, 8): 39.4, (15, 6): 40.0, (7, 8): 39.8, (15, 4): 43.3, (3, 4): 57.4, (5, 8): 42.9},
+    (256, 4096, 4096): {(5, 4): 28.2, (15, 4): 29.1, (7, 4): 28.9, (3, 4): 34.1},
+    (300, 512, 672): {(5, 4): 10.0, (5, 6): 11.2, (5, 2): 10.7, (7, 1): 14.3, (3, 2): 14.5},
+    (1024, 1024, 1024): {(5, 2): 14.0, (5, 4): 14.0, (15, 2): 17.8, (7, 2): 17.7},
+    (128, 28672, 8192): {(15, 2): 80.1, (15, 4): 81.2, (7, 2): 86.3, (5, 2): 99.2},
+    (512, 4096, 4096): {(15, 4): 33.3, (7, 4): 33.5, (5, 4): 37.2},
+}
+
+
+@pytest.mark.parametrize("shape", sorted(MEASURED_TILED_US))
+def test_tiled_plan_within_12pct_of_measured_best(kk, shape):
+    M, N, K = shape
+    kind, variant, split, desc = kk.select_plan(M, N, K, "kn")
+    times = MEASURED_TILED_US[shape]
+    assert kind == kk.KERNEL_TILED
+    assert (variant, split) in times, f"pick {desc} was not measured"
+    assert times[(variant, split)] <= 1.125 * min(times.values()), desc
