@@ -326,11 +326,10 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
       for (int g = 0; g < 2; ++g) {
         u32x2 x, y;
         if constexpr (kG) {
-          // the words of columns 4c + j, j = 0..3, are 16 contiguous bytes
-          const u32x4 v = __builtin_bit_cast(u32x4, g == 0 ? (sub == 0 ? lds_b128<O * 256>(b_off[0])
-                                                                       : lds_b128<O * 256>(b_off[1]))
-                                                           : (sub == 0 ? lds_b128<O * 256 + 256>(b_off[0])
-                                                                       : lds_b128<O * 256 + 256>(b_off[1])));
+          // chunk 4 sub + q (b_off[sub]): the words of columns 4c + j, j =
+          // 0..3, are 16 contiguous bytes; group g is 256 B further
+          const uint32_t base = b_off[sub];
+          const u32x4 v = __builtin_bit_cast(u32x4, g == 0 ? lds_b128<O * 256>(base) : lds_b128<O * 256 + 256>(base));
           r[4 * g + 0] = v.x; r[4 * g + 1] = v.y; r[4 * g + 2] = v.z; r[4 * g + 3] = v.w;
           continue;
         } else if constexpr (kKN) {
