@@ -137,7 +137,12 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
   // kernel, first choice that fits (measured on MI355X at N = 8192 / 28672,
   // K = 8192: 512-K waves with 2 splits beat 256-K waves with 4; both beat
   // this family by 1.3-1.7x).
-  if (layout == kLayoutNK || layout == kLayoutP) {
+  // [N,K/2] with M > 16 and N >= 16384: the GEMV's 128-column CTAs reuse each
+  // activation byte over twice the streaming kernel's columns (M = 24 / 32,
+  // K = 8192: 32.5 / 33.7 us at N = 16384 and 56.4 / 58.5 us at N = 28672,
+  // against 40.0 / 40.5 and 72.9 / 74.2 us streaming; at N = 8192 they tie)
+  const bool wide_gemv = two && layout == kLayoutNK && N >= 16384;
+  if ((layout == kLayoutNK || layout == kLayoutP) && !wide_gemv) {
     // M <= 8: the whole-K kernel first (256-K waves up to K = 4096).  It
     // reads 32 x K activation bytes per CU, which at M = 16 is twice the CU's
     // weight bytes; there the split-K kernel, which reuses each CTA's K range
@@ -170,7 +175,7 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
     // are the faster ones)
     want = two ? 4 : N >= 24576 ? 1 : 0;
   else
-    want = two ? 7 : 6;  // (2,2,16,2) / (1,2,16,4)
+    want = two ? (wide_gemv ? 4 : 7) : 6;  // (2,8,8,2) or (2,2,16,2) / (1,2,16,4)
   const GemvShape& g = kGemv[want];
   const int64_t groups = ceil_div(N, 16 * g.cb);
   const int64_t steps = gemv_steps(layout, K);

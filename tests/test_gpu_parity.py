@@ -261,6 +261,23 @@ def test_stream_whole_rejects(kk, variant, kw, kmax):
             run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=(kk.KERNEL_STREAM, variant, split))
 
 
+@pytest.mark.parametrize("M", [24, 32])
+def test_wide_nk_decode_takes_gemv(kk, M):
+    """[N,K/2], 16 < M <= 32, N >= 16384: the auto plan is the GEMV family
+    (128-column CTAs); checked against the oracle on sampled columns."""
+    import torch
+
+    N, K = 16384, 1024
+    kind, _, _, desc = kk.select_plan(M, N, K, "nk")
+    assert kind == kk.KERNEL_GEMV, desc
+    A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=M + 70)
+    cols = np.sort(np.random.default_rng(M).choice(N, 512, replace=False))
+    ref = oracle_f64(A_bits, W, S, cols=cols)
+    log(f"case wide nk decode M={M} plan={desc}")
+    out = run_gemm(kk, A_bits, W, S, "nk", torch.float32)
+    assert mo.strict_violations(out[:, cols], ref, K) == 0
+
+
 def test_stream_rejects_unsupported(kk):
     import torch
 
