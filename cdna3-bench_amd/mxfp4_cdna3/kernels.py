@@ -152,8 +152,10 @@ def prepack(B_packed, B_scales, layout=LAYOUT_P):
     """Device prepack of reference-layout weights ([K/2, N], [K/32, N]).
 
     layout "g" gives the strategy-G arrays of ref.py:85-101 (flattened, as
-    ``prepack_b_mxfp4`` returns them, ready for ``gemm_g``); "p" (default)
-    the panel layout the MI355X kernels prefer.
+    ``prepack_b_mxfp4`` returns them, ready for ``gemm_g``): the fastest
+    layout for M > 32 (the hand-scheduled tiled kernel reads it directly).
+    "p" (default) gives the panel layout: the fastest for decode shapes
+    (M <= 32, the streaming kernels).
     """
     Bp, Sp = _ext.convert_layout(B_packed, B_scales, LAYOUT_KN, layout, None)
     return (Bp.reshape(-1), Sp.reshape(-1)) if layout == LAYOUT_G else (Bp, Sp)
