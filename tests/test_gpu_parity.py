@@ -414,20 +414,22 @@ def test_baseline_memory_bound_configs(kk, name, layout):
     _check_config(kk, cfg, layout, rows_k=32, cols_k=4096)
 
 
+@pytest.mark.parametrize("layout", ["kn", "nk", "g"])
 @pytest.mark.parametrize("name", ["dit_up", "dit_down"])
-def test_baseline_mfma_bound_configs(kk, name):
+def test_baseline_mfma_bound_configs(kk, name, layout):
+    """Full size in every layout the scheduled kernel reads."""
     import torch
 
     cfg = {c.name: c for c in mo.baseline_configs()}[name]
-    log(f"case config {name}")
-    A_bits, W, S, out = _check_config(kk, cfg, "kn")
+    log(f"case config {name} layout={layout}")
+    A_bits, W, S, out = _check_config(kk, cfg, layout)
     perm = np.random.default_rng(0).permutation(cfg.M)
-    outp = run_gemm(kk, A_bits[perm], W, S, "kn", torch.bfloat16)
+    outp = run_gemm(kk, A_bits[perm], W, S, layout, torch.bfloat16)
     assert np.array_equal(outp, out[perm])
     # linearity in A: 2A -> 2C exactly (power-of-two scaling)
     A2 = mo.f32_to_bf16_bits(2.0 * mo.bf16_bits_to_f32(A_bits))
-    out2 = run_gemm(kk, A2, W, S, "kn", torch.float32)
-    out1 = run_gemm(kk, A_bits, W, S, "kn", torch.float32)
+    out2 = run_gemm(kk, A2, W, S, layout, torch.float32)
+    out1 = run_gemm(kk, A_bits, W, S, layout, torch.float32)
     assert np.array_equal(out2, 2.0 * out1)
 
 
