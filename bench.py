@@ -187,8 +187,8 @@ def main():
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
-        print("bench.py: this build runs on one GPU only; multi-GPU sharding is a design note "
-              "(DESIGN.md), not a measured path. Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this build runs on one GPU only; sharding over several GPUs is "
+              "designed but not built or measured. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch

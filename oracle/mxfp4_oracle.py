@@ -286,7 +286,7 @@ def from_layout(B, S, layout, K, N):
 
 
 # ---------------------------------------------------------------------------
-# Layout transforms (same bytes, transposed)
+# Layout transforms ([N,K/2] <-> [K/2,N]: the same bytes, transposed)
 # ---------------------------------------------------------------------------
 
 def nk_to_kn(W_nk, S_nk):
@@ -439,7 +439,7 @@ def sha256_of(*arrays) -> str:
 
 
 # ---------------------------------------------------------------------------
-# Roofline bookkeeping (algorithmic work; SURVEY 8d formulas)
+# Roofline bookkeeping (algorithmic flops and HBM bytes per launch)
 # ---------------------------------------------------------------------------
 
 def gemm_flops(M, N, K) -> float:

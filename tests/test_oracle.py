@@ -217,7 +217,8 @@ def test_torch_cpu_path_matches_f64_oracle():
 
 
 def test_wide_exponent_sweep_needs_cancellation_bound():
-    """SURVEY H1 on a sample of the 70B sweep: an fp32 GEMM passes the
+    """The wide-exponent tolerance question on a sample of the 70B sweep
+    (E8M0 exponents 110..140, where products of large scales cancel): an fp32 GEMM passes the
     cancellation-aware bound (c = 4) even where the strict bound is not
     guaranteed."""
     pytest.importorskip("torch")
