@@ -575,8 +575,9 @@ void launch_sched_layout(const TiledArgs& args, int grid, hipStream_t stream) {
 }
 
 hipError_t launch_tiled_sched(int layout, const TiledShape& shape, const TiledArgs& args, hipStream_t stream) {
-  // [N,K/2] reads each column's scales as aligned dwords of K-step pairs
-  const int kmod = layout == kLayoutKN ? kBK : 2 * kBK;
+  // [N,K/2] reads each column's scales as aligned dwords of K-step pairs;
+  // [K/2,N] and G move whole 64-K steps
+  const int kmod = layout == kLayoutNK ? 2 * kBK : kBK;
   if (!tiled_sched_available(layout, shape) || args.K % kmod != 0) return hipErrorInvalidValue;
   const int grid = args.tiles_m * args.tiles_n * args.splits;
   if (layout == kLayoutKN)

@@ -178,6 +178,25 @@ def test_sched_kernel_tails_and_splits(kk, layout, M, N, K):
             np.testing.assert_allclose(out, base, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
 
 
+@pytest.mark.parametrize("K", [192, 448, 1600])
+def test_sched_g_odd_step_counts(kk, K):
+    """G weights with an odd number of 64-K steps (K % 128 == 64): the G
+    loader moves whole 64-K steps, so the scheduled kernel takes these K
+    (only [N,K/2] pairs steps for its scale dwords).  Auto plan and explicit
+    splits, against the float64 oracle and the [K/2,N] result."""
+    import torch
+
+    M, N = 200, 768
+    A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=K)
+    ref = oracle_f64(A_bits, W, S)
+    for plan in [None] + [(kk.KERNEL_TILED, SCHED_VARIANT, s) for s in (1, 2, 3) if s <= K // 64]:
+        log(f"case sched g K={K} plan={plan}")
+        out = run_gemm(kk, A_bits, W, S, "g", torch.float32, plan=plan)
+        assert mo.strict_violations(out, ref, K) == 0, f"plan {plan}"
+        if plan is not None:
+            assert np.array_equal(out, run_gemm(kk, A_bits, W, S, "kn", torch.float32, plan=plan)), f"plan {plan}"
+
+
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 @pytest.mark.parametrize("M", [1, 16, 29])
 def test_every_gemv_variant_and_split(kk, layout, M):
