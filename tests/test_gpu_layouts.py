@@ -130,6 +130,23 @@ def test_tiled_prepacked_equals_base_layout(kk, pre, base, K):
             assert mo.strict_violations(a, ref, K) == 0
 
 
+@pytest.mark.parametrize("M", [16, 300])
+def test_tiled_p_odd_step_count(kk, M):
+    """P weights with K % 128 == 64 (an odd number of 64-K panels): the
+    pipelined kernel reads P scales per panel, so it takes these K; the
+    streaming kernels need K % 256 and leave them to it.  Auto plan and every
+    pipelined variant, against the float64 oracle."""
+    import torch
+
+    N, K = 512, 576
+    A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=41)
+    ref = oracle_f64(A_bits, W, S)
+    for plan in [None] + [(kk.KERNEL_TILED, v, s) for v in PIPE_VARIANTS for s in (1, 3)]:
+        log(f"case tiled p M={M} K={K} plan={plan}")
+        out = run_gemm(kk, A_bits, W, S, "p", torch.float32, plan=plan)
+        assert mo.strict_violations(out, ref, K) == 0, f"plan {plan}"
+
+
 def test_tiled_rejects_prepacked_without_loader(kk):
     import torch
 
