@@ -196,11 +196,14 @@ double tiled_eff(const TiledVariant& v, int layout) {
 // Tiled variants a layout may use: the first tiled kernel has only the plain
 // loaders, the scheduled kernel the plain and G ones ([N,K/2]: aligned scale
 // dwords of K-step pairs), the pipelined kernel all four (its [N,K/2] loader
-// reads aligned scale dwords).
-bool tiled_variant_ok(const TiledVariant& v, int layout, int64_t K) {
+// reads aligned scale dwords).  The scheduled kernel stores 4 adjacent
+// columns per lane and row (8 / 16 bytes): [N,K/2] needs N % 4 == 0 there
+// ([K/2,N] has N % 16 == 0 and G N % 128 == 0 already), so that every group
+// of 4 is inside the row and aligned.
+bool tiled_variant_ok(const TiledVariant& v, int layout, int64_t N, int64_t K) {
   if (v.family == kFamilyPlain) return layout == kLayoutKN || layout == kLayoutNK;
   if (v.family == kFamilySched)
-    return K % (layout == kLayoutNK ? 128 : 64) == 0 && tiled_sched_available(layout, v.shape);
+    return K % (layout == kLayoutNK ? 128 : 64) == 0 && N % 4 == 0 && tiled_sched_available(layout, v.shape);
   if (layout == kLayoutNK) return K % 128 == 0;
   if (layout == kLayoutG) return v.shape.bn() % kGCols == 0;
   return true;
@@ -243,7 +246,7 @@ void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) 
   const int64_t ksteps = ceil_div(K, 64);
   for (int v = 0; v < kNumTiled; ++v) {
     const TiledVariant& tv = kTiled[v];
-    if (!tiled_variant_ok(tv, layout, K) || tiled_eff(tv, layout) <= 0.0) continue;
+    if (!tiled_variant_ok(tv, layout, N, K) || tiled_eff(tv, layout) <= 0.0) continue;
     const int64_t tiles = ceil_div(M, tv.shape.bm()) * ceil_div(N, tv.shape.bn());
     for (int s = 1; s <= 16 && s <= ksteps; ++s) {
       if (s > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) break;
@@ -285,7 +288,7 @@ hipError_t validate_plan(int layout, int64_t M, int64_t N, int64_t K, const mxfp
     case MXFP4_KERNEL_TILED: {
       if (p.variant < 0 || p.variant >= kNumTiled) return hipErrorInvalidValue;
       if (layout == kLayoutKN && N % 16 != 0) return hipErrorInvalidValue;
-      if (!tiled_variant_ok(kTiled[p.variant], layout, K)) return hipErrorInvalidValue;
+      if (!tiled_variant_ok(kTiled[p.variant], layout, N, K)) return hipErrorInvalidValue;
       const TiledShape& s = kTiled[p.variant].shape;
       const int64_t tiles = ceil_div(M, s.bm()) * ceil_div(N, s.bn());
       if (p.split_k > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) return hipErrorInvalidValue;

@@ -579,6 +579,8 @@ hipError_t launch_tiled_sched(int layout, const TiledShape& shape, const TiledAr
   // [K/2,N] and G move whole 64-K steps
   const int kmod = layout == kLayoutNK ? 2 * kBK : kBK;
   if (!tiled_sched_available(layout, shape) || args.K % kmod != 0) return hipErrorInvalidValue;
+  // the store writes 4 adjacent columns per lane and row
+  if (args.N % 4 != 0) return hipErrorInvalidValue;
   const int grid = args.tiles_m * args.tiles_n * args.splits;
   if (layout == kLayoutKN)
     launch_sched_layout<kLayoutKN>(args, grid, stream);

@@ -178,6 +178,28 @@ def test_sched_kernel_tails_and_splits(kk, layout, M, N, K):
             np.testing.assert_allclose(out, base, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
 
 
+@pytest.mark.parametrize("N", [514, 260, 42])
+def test_tiled_nk_column_tails(kk, N):
+    """[N,K/2] weights with N % 16 != 0 on the tiled kernels.  The scheduled
+    kernel stores 4 adjacent columns per lane and row, so it takes N % 4 == 0
+    only (N = 514 and 42 are rejected before launch, and the auto plan picks
+    a kernel with per-column stores); the others store per column.  Every
+    variant that takes the shape, and the auto plan, against the oracle."""
+    import torch
+
+    M, K = 300, 640
+    A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=N)
+    ref = oracle_f64(A_bits, W, S)
+    for plan in [None] + [(kk.KERNEL_TILED, v, s) for v in TILED_VARIANTS for s in (1, 3)]:
+        log(f"case tiled nk column tail N={N} plan={plan}")
+        if plan is not None and plan[1] == SCHED_VARIANT and N % 4:
+            with pytest.raises(RuntimeError, match="invalid argument"):
+                run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan)
+            continue
+        out = run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan)
+        assert mo.strict_violations(out, ref, K) == 0, f"plan {plan}"
+
+
 @pytest.mark.parametrize("K", [192, 448, 1600])
 def test_sched_g_odd_step_counts(kk, K):
     """G weights with an odd number of 64-K steps (K % 128 == 64): the G
