@@ -366,6 +366,7 @@ hipError_t make_epilogue(const mxfp4_epilogue* in, Epilogue* out) {
   out->res_bf16 = in->residual_dtype == MXFP4_OUT_BF16;
   out->act = in->activation;
   out->any = in->bias != nullptr || in->residual != nullptr || in->activation != MXFP4_ACT_NONE;
+  out->res_vec = ((uintptr_t)in->residual & (in->residual_dtype == MXFP4_OUT_BF16 ? 7u : 15u)) == 0;
   return hipSuccess;
 }
 

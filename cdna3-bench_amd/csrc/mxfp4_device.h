@@ -235,16 +235,23 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_
 // ---- fused epilogue -----------------------------------------------------------
 // v = act(acc + bias[col]) + residual[row][col], in fp32 (the definitions of
 // torch.nn.functional.silu / gelu / gelu(approximate="tanh")).
+template <int ACT>
+__device__ __forceinline__ float activate_c(float v) {
+  if constexpr (ACT == 1)  // SiLU
+    return v / (1.0f + expf(-v));
+  else if constexpr (ACT == 2)  // GELU (erf)
+    return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+  else if constexpr (ACT == 3)  // GELU (tanh)
+    return 0.5f * v * (1.0f + tanhf(0.79788456080286536f * (v + 0.044715f * v * v * v)));
+  else
+    return v;
+}
 __device__ __forceinline__ float activate(int act, float v) {
   switch (act) {
-    case 1:  // SiLU
-      return v / (1.0f + expf(-v));
-    case 2:  // GELU (erf)
-      return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-    case 3:  // GELU (tanh)
-      return 0.5f * v * (1.0f + tanhf(0.79788456080286536f * (v + 0.044715f * v * v * v)));
-    default:
-      return v;
+    case 1: return activate_c<1>(v);
+    case 2: return activate_c<2>(v);
+    case 3: return activate_c<3>(v);
+    default: return v;
   }
 }
 

@@ -17,6 +17,7 @@ struct Epilogue {
   int bias_bf16 = 0, res_bf16 = 0;
   int act = 0;                     // MXFP4_ACT_*
   int any = 0;                     // any term present (else the plain store)
+  int res_vec = 0;                 // residual aligned for 4-element vector reads (8 B bf16, 16 B fp32)
 };
 
 // Tiled MFMA family (M > 32): BM x BN x 64 tiles, WM x WN waves, each wave

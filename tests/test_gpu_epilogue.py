@@ -128,6 +128,29 @@ def test_epilogue_k0_and_residual_is_c(kk):
         assert torch.allclose(C, plain + old, rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("plan", [(2, 15, 1), (2, 15, 3), (2, 7, 1)])
+def test_epilogue_unaligned_residual(kk, plan):
+    """A residual view one element into its buffer (4-byte aligned fp32,
+    2-byte aligned bf16): the scheduled kernel reads it per element instead
+    of as 4-element vectors; C is bit-identical to the aligned residual's."""
+    import torch
+
+    M, N, K = 300, 512, 640
+    A_bits, W, S = mo.make_inputs(M, N, K, 120, 128, seed=5)
+    B, Sc = weights_for_layout(W, S, "kn")
+    A, Bd, Sd = to_dev_bf16(A_bits), to_dev_u8(B), to_dev_u8(Sc)
+    bias = torch.randn(N, device="cuda")
+    for dt in (torch.float32, torch.bfloat16):
+        buf = torch.randn(M * N + 1, device="cuda").to(dt)
+        shifted = buf[1:].view(M, N)
+        aligned = shifted.clone()
+        assert shifted.data_ptr() % 8 != 0
+        log(f"case epilogue unaligned residual plan={plan} dtype={dt}")
+        want = kk.gemm(A, Bd, Sd, None, "kn", torch.float32, plan, bias, "gelu_tanh", aligned)
+        got = kk.gemm(A, Bd, Sd, None, "kn", torch.float32, plan, bias, "gelu_tanh", shifted)
+        assert torch.equal(got, want)
+
+
 def test_epilogue_argument_errors(kk):
     import torch
 
