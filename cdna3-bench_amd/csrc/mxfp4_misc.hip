@@ -122,12 +122,15 @@ __global__ void __launch_bounds__(256) convert_scales_kernel(const uint8_t* __re
   out[o] = S[scale_offset<SRC>(g, n, K, N)];
 }
 
+// 16 bytes per thread; vector stores when p is 16-byte aligned (C may be a
+// view at any element offset), byte stores otherwise and for the tail.
 __global__ void __launch_bounds__(256) zero_fill_kernel(uint8_t* p, size_t bytes) {
   const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
-  if (i + 16 <= bytes) {
+  if (i + 16 <= bytes && ((uintptr_t)p & 15u) == 0) {
     *reinterpret_cast<u32x4*>(p + i) = u32x4{0u, 0u, 0u, 0u};
   } else {
-    for (size_t j = i; j < bytes; ++j) p[j] = 0;
+    const size_t end = i + 16 < bytes ? i + 16 : bytes;
+    for (size_t j = i; j < end; ++j) p[j] = 0;
   }
 }
 

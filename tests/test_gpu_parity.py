@@ -376,6 +376,14 @@ def test_empty_and_k0(kk):
                        torch.zeros(0, 128, dtype=torch.uint8, device="cuda"), C)
     torch.cuda.synchronize()
     assert torch.all(out == 0)
+    # C a view at an odd bf16 offset (not 16-byte aligned): all of C cleared,
+    # the elements on either side kept
+    buf = torch.full((4 * 130 + 2,), 5.0, dtype=torch.bfloat16, device="cuda")
+    Cv = buf[1:1 + 4 * 130].view(4, 130)
+    kk.gemm(A, torch.zeros(0, 130, dtype=torch.uint8, device="cuda"),
+            torch.zeros(0, 130, dtype=torch.uint8, device="cuda"), Cv, "kn")
+    torch.cuda.synchronize()
+    assert torch.all(buf[1:-1] == 0) and buf[0].item() == 5.0 and buf[-1].item() == 5.0
 
 
 # --------------------------------------------------------------------------- reference API
