@@ -199,11 +199,15 @@ double tiled_eff(const TiledVariant& v, int layout) {
 // reads aligned scale dwords).  The scheduled kernel stores 4 adjacent
 // columns per lane and row (8 / 16 bytes): [N,K/2] needs N % 4 == 0 there
 // ([K/2,N] has N % 16 == 0 and G N % 128 == 0 already), so that every group
-// of 4 is inside the row and aligned.
+// of 4 is inside the row and aligned.  Its [K/2,N] loader addresses the
+// whole K range of a column block from one buffer descriptor (the K step is
+// the scalar offset), so the codes must fit the descriptor's range; larger
+// [K/2,N] weights take the kernels that rebase per K step.
 bool tiled_variant_ok(const TiledVariant& v, int layout, int64_t N, int64_t K) {
   if (v.family == kFamilyPlain) return layout == kLayoutKN || layout == kLayoutNK;
   if (v.family == kFamilySched)
-    return K % (layout == kLayoutNK ? 128 : 64) == 0 && N % 4 == 0 && tiled_sched_available(layout, v.shape);
+    return K % (layout == kLayoutNK ? 128 : 64) == 0 && N % 4 == 0 &&
+           (layout != kLayoutKN || tiled_sched_kn_fits(N, K)) && tiled_sched_available(layout, v.shape);
   if (layout == kLayoutNK) return K % 128 == 0;
   if (layout == kLayoutG) return v.shape.bn() % kGCols == 0;
   return true;

@@ -88,6 +88,8 @@ bool tiled_pipe_shape_available(int layout, const TiledShape& shape);
 hipError_t launch_tiled_sched(int layout, const TiledShape& shape, const TiledArgs& args,
                               hipStream_t stream);
 bool tiled_sched_available(int layout, const TiledShape& shape);
+// [K/2,N] codes (and scales) within the scheduled kernel's 1 GiB descriptor range
+bool tiled_sched_kn_fits(int64_t N, int64_t K);
 
 hipError_t launch_gemv(int layout, const GemvShape& shape, const GemvArgs& args,
                        hipStream_t stream);

@@ -610,6 +610,12 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
 
 }  // namespace
 
+bool tiled_sched_kn_fits(int64_t N, int64_t K) {
+  // the largest offset from B + n0 is (K/2 - 1) * N + 255 (+ 16 for the
+  // DMA's own bytes)
+  return (K / 2) * N + 256 <= (int64_t)kNumRecords;
+}
+
 bool tiled_sched_available(int layout, const TiledShape& s) {
   return (layout == kLayoutKN || layout == kLayoutNK || layout == kLayoutG) && s.bm() == kBM && s.bn() == kBN &&
          s.wm * s.wn == kWaves && s.stages == kNS;
@@ -638,6 +644,7 @@ hipError_t launch_tiled_sched(int layout, const TiledShape& shape, const TiledAr
   if (!tiled_sched_available(layout, shape) || args.K % kmod != 0) return hipErrorInvalidValue;
   // the store writes 4 adjacent columns per lane and row
   if (args.N % 4 != 0) return hipErrorInvalidValue;
+  if (layout == kLayoutKN && !tiled_sched_kn_fits(args.N, args.K)) return hipErrorInvalidValue;
   const int grid = args.tiles_m * args.tiles_n * args.splits;
   if (layout == kLayoutKN)
     launch_sched_layout<kLayoutKN>(args, grid, stream);

@@ -200,6 +200,34 @@ def test_tiled_nk_column_tails(kk, N):
         assert mo.strict_violations(out, ref, K) == 0, f"plan {plan}"
 
 
+def test_kn_weights_of_one_gib(kk):
+    """[K/2,N] codes of exactly 1 GiB (K = 32768, N = 65536): past the
+    scheduled kernel's descriptor range, so an explicit scheduled plan is
+    rejected and the auto plan takes a kernel that rebases per K step; C
+    against the float64 oracle on sampled rows and columns (edges included)."""
+    import torch
+
+    M, N, K = 300, 65536, 32768
+    rng = np.random.default_rng(7)
+    A_bits = mo.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    W = rng.integers(0, 256, size=(N, K // 2), dtype=np.uint8)  # uniform E2M1 codes
+    S = rng.integers(122, 131, size=(N, K // 32), dtype=np.uint8)
+    Bkn, Skn = mo.nk_to_kn(W, S)
+    A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(Bkn), to_dev_u8(Skn)
+    del Bkn
+    kind, variant, split, desc = kk.select_plan(M, N, K, "kn")
+    log(f"case kn 1 GiB auto plan {desc}")
+    assert not desc.startswith("tiled-sched")
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        kk.gemm(A, B, Sd, None, "kn", torch.float32, (kk.KERNEL_TILED, SCHED_VARIANT, 1))
+    out = kk.gemm(A, B, Sd, None, "kn", torch.float32)
+    torch.cuda.synchronize()
+    rows, cols = sample_indices(M, 6, rng), sample_indices(N, 40, rng)
+    got = out[torch.from_numpy(rows).cuda()][:, torch.from_numpy(cols).cuda()].cpu().numpy()
+    ref = oracle_f64(A_bits, W, S, rows=rows, cols=cols)
+    assert mo.strict_violations(got, ref, K) == 0
+
+
 @pytest.mark.parametrize("K", [192, 448, 1600])
 def test_sched_g_odd_step_counts(kk, K):
     """G weights with an odd number of 64-K steps (K % 128 == 64): the G
