@@ -27,7 +27,8 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 
 def build_library(jobs: int = 8) -> str:
-    subprocess.run(["make", "-s", "-C", CSRC, f"-j{jobs}", f"OUT_DIR={PKG}"], check=True)
+    # -B: every call compiles every source, also over an existing build
+    subprocess.run(["make", "-B", "-s", "-C", CSRC, f"-j{jobs}", f"OUT_DIR={PKG}"], check=True)
     return os.path.join(PKG, "libmxfp4_mi355x.so")
 
 
