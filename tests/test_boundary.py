@@ -225,3 +225,22 @@ def test_tiled_plan_within_12pct_of_measured_best(kk, shape):
     assert kind == kk.KERNEL_TILED
     assert (variant, split) in times, f"pick {desc} was not measured"
     assert times[(variant, split)] <= 1.125 * min(times.values()), desc
+
+
+@pytest.mark.parametrize("M,N,K,layout,sched", [
+    (512, 4098, 4096, "nk", False),    # N % 4 == 2: the scheduled kernel's 4-column stores would leave the row
+    (512, 4100, 4096, "nk", True),     # N % 4 == 0
+    (4096, 65536, 32768, "kn", False),  # [K/2,N] codes of 1 GiB: past the scheduled kernel's descriptor range
+    (4096, 65536, 32768, "g", True),   # G spans are per column block
+    (4096, 65520, 32768, "kn", True),  # just under 1 GiB
+])
+def test_scheduled_kernel_shape_rules(kk, lib, M, N, K, layout, sched):
+    """The selector never hands the scheduled kernel a shape it cannot
+    address or store, and explicit scheduled plans for such shapes are
+    rejected by the host-side validation (a valid split-2 plan needs a
+    workspace; a rejected one reports 0 bytes)."""
+    desc = kk.select_plan(M, N, K, layout)[3]
+    assert desc.startswith("tiled-sched") == sched, desc
+    code = {"kn": 0, "nk": 1, "g": 2}[layout]
+    ws = lib.mxfp4_gemm_workspace_bytes(M, N, K, code, ctypes.byref(Plan(2, 15, 2, 0)))
+    assert (ws > 0) == sched, ws
