@@ -91,6 +91,7 @@ const StreamShape kStream[] = {
 };
 constexpr int kNumStream = sizeof(kStream) / sizeof(kStream[0]);
 constexpr int kStreamSpin = 4096;  // late-unit polls before counter arbitration
+constexpr int64_t kRsrcBytes = 1LL << 30;  // range of one buffer descriptor (mxfp4_device.h kNumRecords)
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -110,6 +111,9 @@ bool stream_plan_ok(int layout, int64_t M, int64_t N, int64_t K, const StreamSha
   const int64_t splits = stream_splits(s, K);
   if (splits > s.smax) return false;
   if (splits > 1 && stream_ctas(s, N, K) * 4 > (int64_t)MXFP4_COUNTER_BYTES) return false;
+  // the split-K packets are addressed through one buffer descriptor over the
+  // partials (32-bit offsets, kNumRecords bytes)
+  if (splits > 1 && stream_ctas(s, N, K) * splits * s.tile() * 8 > kRsrcBytes) return false;
   return stream_shape_available(s);
 }
 
@@ -184,7 +188,7 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
   out->kernel = MXFP4_KERNEL_GEMV;
   out->variant = want;
   out->split_k = (int32_t)splits;
-  out->reserved = 0;
+  out->flags = 0;
 }
 
 // The G loader uses the [K/2,N] lane map and the panel loader the [N,K/2]
@@ -265,11 +269,12 @@ void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) 
   out->kernel = MXFP4_KERNEL_TILED;
   out->variant = bv;
   out->split_k = bs;
-  out->reserved = 0;
+  out->flags = 0;
 }
 
 hipError_t validate_plan(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_plan& p) {
   if (p.split_k < 1) return hipErrorInvalidValue;
+  if (p.flags & ~MXFP4_PLAN_STREAM_NO_POLL) return hipErrorInvalidValue;
   switch (p.kernel) {
     case MXFP4_KERNEL_GENERIC:
       return hipSuccess;
@@ -442,7 +447,7 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
       a.ctas = (int)stream_ctas(s, N, K);
       a.partials = a.splits > 1 ? partials : nullptr;
       a.counters = a.splits > 1 ? counters : nullptr;
-      a.spin_limit = kStreamSpin;
+      a.spin_limit = (plan.flags & MXFP4_PLAN_STREAM_NO_POLL) ? 0 : kStreamSpin;
       a.ep = ep;
       return launch_stream(layout, s, a, stream);
     }
@@ -577,8 +582,6 @@ hipError_t mxfp4_convert_layout(const uint8_t* B, const uint8_t* S, int src_layo
   if (!layout_ok(src_layout, N, K) || !layout_ok(dst_layout, N, K)) return hipErrorInvalidValue;
   if (K * N == 0) return hipSuccess;
   if (!B || !S || !B_out || !S_out || !aligned16(B_out)) return hipErrorInvalidValue;
-  // one thread per 16 code bytes / per scale byte, 256 per block
-  if ((uint64_t)(K / 32) * (uint64_t)N / 256 >= (1ull << 31)) return hipErrorInvalidValue;
   const uint64_t code_bytes = (uint64_t)K / 2 * N, scale_bytes = (uint64_t)K / 32 * N;
   const uint64_t b0 = (uintptr_t)B, b1 = b0 + code_bytes, o0 = (uintptr_t)B_out, o1 = o0 + code_bytes;
   const uint64_t s0 = (uintptr_t)S, s1 = s0 + scale_bytes, t0 = (uintptr_t)S_out, t1 = t0 + scale_bytes;

@@ -5,11 +5,13 @@
 //   csrc/strategy_h_dequant.h:24-67   (unscaled perm dequant)      -> fp4x2_to_bf16x2 (scaled cvt)
 //   csrc/direct_lds.h:14-17           (VGPR-staged "direct" load)  -> buffer_load_lds16
 //   csrc/bf16_gemm.h:18-20            (mfma 16x16x16 bf16)         -> mfma_32x32x16 / mfma_16x16x32
-//   csrc/bf16_gemm.h:156-175          (6-XCD remap, props/launch)  -> xcd_chunked_id (8 XCDs)
+//   csrc/bf16_gemm.h:156-175          (6-XCD remap, props/launch)  -> xcd_chunked_id, tile_of (mxfp4_schedule.h)
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "mxfp4_schedule.h"
 
 namespace mxfp4 {
 
@@ -24,7 +26,6 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr int kGroup = 32;  // K elements per E8M0 scale
 constexpr int kWave = 64;   // CDNA wavefront width
-constexpr int kNumXcds = 8; // MI355X: 8 XCDs x 32 CUs
 
 // Offset given to a masked lane of a buffer load: past num_records, so the
 // hardware returns zeros (and writes zeros to LDS for the LDS-DMA form).
@@ -211,15 +212,6 @@ __device__ __forceinline__ void splitk_sum(__amdgpu_buffer_rsrc_t rp, uint32_t s
 #pragma unroll
     for (int b = 0; b < GRP; ++b) put(g0 + b, sum[b]);
   }
-}
-
-// Workgroups are dispatched round-robin over the XCDs (id % 8).  Renumber so
-// each XCD owns one contiguous range of logical ids; a bijection for any
-// count.  Neighbouring logical tiles then share an XCD's L2.
-__device__ __forceinline__ int xcd_chunked_id(int id, int count) {
-  const int q = count / kNumXcds, r = count % kNumXcds;
-  const int x = id % kNumXcds, local = id / kNumXcds;
-  return x * q + (x < r ? x : r) + local;
 }
 
 __device__ __forceinline__ uint32_t bf16_bits_rne(float f) {

@@ -18,29 +18,40 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
 
+#include <map>
 #include <mutex>
 #include <string>
-#include <unordered_map>
+#include <utility>
 
 #include "mxfp4_mi355x.h"
 
 namespace {
 
-// Per-device workspace: zero-filled on allocation (split-K counters must start
-// at zero; the kernels leave them at zero), grown on demand.
+// Split-K workspace per (device, stream): zero-filled on allocation (split-K
+// counters and packets must start at zero; every call leaves them at zero)
+// and grown on demand.  Calls on one stream run in order, so a stream's
+// workspace is never used by two kernels at once.  A grown-out buffer goes
+// back to torch's caching allocator, which hands it out again only in the
+// order of the stream it was allocated on (this one).  Allocation is refused
+// while the stream captures a graph: the zero fill would only be recorded.
 std::mutex g_ws_mutex;
-std::unordered_map<int, torch::Tensor> g_ws;
+std::map<std::pair<int, hipStream_t>, torch::Tensor> g_ws;
 
-torch::Tensor workspace_for(const torch::Tensor& like, size_t bytes) {
+torch::Tensor workspace_for(const torch::Tensor& like, hipStream_t stream, size_t bytes) {
   if (bytes == 0) return torch::Tensor();
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  const int dev = like.get_device();
-  auto it = g_ws.find(dev);
+  const auto key = std::make_pair((int)like.get_device(), stream);
+  auto it = g_ws.find(key);
   if (it == g_ws.end() || (size_t)it->second.numel() < bytes) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    TORCH_CHECK(hipStreamIsCapturing(stream, &status) == hipSuccess, "hipStreamIsCapturing failed");
+    TORCH_CHECK(status == hipStreamCaptureStatusNone,
+                "mxfp4_cdna3: this call needs a ", bytes, "-byte split-K workspace on the capturing stream; "
+                "run it once on that stream before the graph capture (the workspace is kept per stream)");
     size_t want = bytes;
     if (it != g_ws.end()) want = std::max(bytes, (size_t)it->second.numel() * 2);
-    g_ws[dev] = torch::zeros({(int64_t)want}, like.options().dtype(at::kByte));
-    it = g_ws.find(dev);
+    g_ws[key] = torch::zeros({(int64_t)want}, like.options().dtype(at::kByte));
+    it = g_ws.find(key);
   }
   return it->second;
 }
@@ -97,7 +108,7 @@ void launch(const char* name, const torch::Tensor& A, const torch::Tensor& B,
             const torch::Tensor& S, torch::Tensor& C, int64_t M, int64_t N, int64_t K, int layout,
             const mxfp4_plan* plan, hipStream_t stream, const mxfp4_epilogue* ep = nullptr) {
   const size_t ws_bytes = mxfp4_gemm_workspace_bytes(M, N, K, layout, plan);
-  torch::Tensor ws = workspace_for(A, ws_bytes);
+  torch::Tensor ws = workspace_for(A, stream, ws_bytes);
   hipError_t err = mxfp4_gemm_ex(A.data_ptr(), static_cast<const uint8_t*>(B.data_ptr()),
                                  static_cast<const uint8_t*>(S.data_ptr()), C.data_ptr(), out_code(C), M, N,
                                  K, layout, plan, ep, ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream);
@@ -140,6 +151,12 @@ mxfp4_epilogue make_epilogue(const torch::Tensor& C, int64_t M, int64_t N, const
     ep.residual_dtype = dtype_code(r, "residual");
   }
   return ep;
+}
+
+// (kernel, variant, split_k[, flags]) of the Python API.
+mxfp4_plan plan_from(const std::vector<int64_t>& v) {
+  TORCH_CHECK(v.size() == 3 || v.size() == 4, "plan must be (kernel, variant, split_k[, flags])");
+  return mxfp4_plan{(int32_t)v[0], (int32_t)v[1], (int32_t)v[2], v.size() == 4 ? (int32_t)v[3] : 0};
 }
 
 // Reference dispatch (csrc/mxfp4_ext.cpp:36-48): C=None -> fp32 [M, N].
@@ -222,12 +239,7 @@ torch::Tensor gemm(const torch::Tensor& A, const torch::Tensor& B, const torch::
   torch::Tensor C = C_opt.has_value() ? *C_opt : torch::empty({M, N}, A.options().dtype(dt));
   auto stream = check_inputs(A, B, S, C, M, N, K, lay);
   mxfp4_plan p{MXFP4_KERNEL_AUTO, 0, 1, 0};
-  if (plan.has_value()) {
-    TORCH_CHECK(plan->size() == 3, "plan must be (kernel, variant, split_k)");
-    p.kernel = (int32_t)(*plan)[0];
-    p.variant = (int32_t)(*plan)[1];
-    p.split_k = (int32_t)(*plan)[2];
-  }
+  if (plan.has_value()) p = plan_from(*plan);
   const mxfp4_epilogue ep = make_epilogue(C, M, N, bias, activation, residual);
   launch("mxfp4_gemm", A, B, S, C, M, N, K, lay, &p, stream, &ep);
   return C;
@@ -380,6 +392,14 @@ torch::Tensor dequant(const torch::Tensor& B, const torch::Tensor& S, const std:
   return out;
 }
 
+std::string describe_plan(const std::vector<int64_t>& plan) {
+  const mxfp4_plan p = plan_from(plan);
+  char buf[128];
+  hipError_t err = mxfp4_plan_describe(&p, buf, sizeof(buf));
+  TORCH_CHECK(err == hipSuccess, "mxfp4_plan_describe: ", hipGetErrorString(err));
+  return std::string(buf);
+}
+
 py::tuple select_plan(int64_t M, int64_t N, int64_t K, const std::string& layout) {
   mxfp4_plan p{};
   hipError_t err = mxfp4_select_plan(M, N, K, layout_code(layout), &p);
@@ -436,6 +456,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("quantize", &quantize, py::arg("X"), py::arg("axis") = -1, py::arg("layout") = py::none());
   m.def("convert_layout", &convert_layout, py::arg("B"), py::arg("S"), py::arg("src"), py::arg("dst"),
         py::arg("K") = py::none());
+  m.def("describe_plan", &describe_plan, py::arg("plan"));
   m.def("select_plan", &select_plan, py::arg("M"), py::arg("N"), py::arg("K"), py::arg("layout") = "kn");
   m.def("device_info", &device_info, py::arg("dev_id") = 0);
   m.def("shape_supported_c", [](int64_t M, int64_t N, int64_t K) { return shape_supported('c', M, N, K); },

@@ -14,6 +14,24 @@
 namespace mxfp4 {
 namespace {
 
+// Scale byte 0xFF has no finite value: ref.py:69 computes 2**128 in float64
+// and casts it to float32 (+inf), so codes 0 and 8 (+-0) give NaN and every
+// other code +-inf.  The scaled convert gives NaN for all of them (OCP MX
+// treats 0xFF as NaN), so the dequant tile substitutes the reference's bf16
+// patterns per nibble; exact in fp32 too (bf16 << 16).
+__device__ inline uint32_t e8m0_nan_pair(uint32_t byte) {
+  auto one = [](uint32_t c) -> uint32_t { return (c & 7u) == 0 ? 0x7FC0u : (c & 8u) ? 0xFF80u : 0x7F80u; };
+  return one(byte & 15u) | (one(byte >> 4) << 16);
+}
+
+// Grid-stride loops over `total` items: launches cap the grid at kMaxBlocks
+// blocks of 256 threads, so any size fits the grid limits.
+constexpr unsigned kMaxBlocks = 1u << 20;
+inline unsigned grid_for(size_t items) {
+  const size_t blocks = (items + 255) / 256;
+  return (unsigned)(blocks < kMaxBlocks ? blocks : kMaxBlocks);
+}
+
 // One thread per packed byte (two K-adjacent codes of one column), in
 // [K/2, N] order so the writes stay coalesced; the source positions follow
 // the weight layout (mxfp4_layout.h).
@@ -22,46 +40,50 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict_
                                                       const uint8_t* __restrict__ S, void* out,
                                                       int out_bf16, int K, int N) {
   const size_t total = (size_t)(K / 2) * N;
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const size_t r = idx / N, n = idx - r * N;
-  const uint32_t byte = B[code_offset<LAYOUT>(r, n, K, N)];
-  const uint32_t sbyte = S[scale_offset<LAYOUT>(r / 16, n, K, N)];
-  const uint32_t v = fp4x2_to_bf16x2<0>(byte, e8m0_to_f32(sbyte));
-  const size_t o0 = (2 * r) * (size_t)N + n, o1 = o0 + N;
-  if (out_bf16) {
-    static_cast<uint16_t*>(out)[o0] = (uint16_t)(v & 0xFFFFu);
-    static_cast<uint16_t*>(out)[o1] = (uint16_t)(v >> 16);
-  } else {
-    static_cast<float*>(out)[o0] = __builtin_bit_cast(float, v << 16);
-    static_cast<float*>(out)[o1] = __builtin_bit_cast(float, v & 0xFFFF0000u);
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+      const size_t r = idx / N, n = idx - r * N;
+      const uint32_t byte = B[code_offset<LAYOUT>(r, n, K, N)];
+      const uint32_t sbyte = S[scale_offset<LAYOUT>(r / 16, n, K, N)];
+      uint32_t v = fp4x2_to_bf16x2<0>(byte, e8m0_to_f32(sbyte));
+      if (sbyte == 0xFFu) v = e8m0_nan_pair(byte);
+      const size_t o0 = (2 * r) * (size_t)N + n, o1 = o0 + N;
+      if (out_bf16) {
+        static_cast<uint16_t*>(out)[o0] = (uint16_t)(v & 0xFFFFu);
+        static_cast<uint16_t*>(out)[o1] = (uint16_t)(v >> 16);
+      } else {
+        static_cast<float*>(out)[o0] = __builtin_bit_cast(float, v << 16);
+        static_cast<float*>(out)[o1] = __builtin_bit_cast(float, v & 0xFFFF0000u);
+      }
+    }
   }
-}
 
-// One thread per output element; fp32 accumulation in K order.
+  // One thread per output element; fp32 accumulation in K order.
 template <int LAYOUT>
 __global__ void __launch_bounds__(256) generic_kernel(const uint16_t* __restrict__ A,
                                                       const uint8_t* __restrict__ B,
                                                       const uint8_t* __restrict__ S, void* C,
                                                       int out_bf16, int M, int N, int K, Epilogue ep) {
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (size_t)M * N) return;
-  const int m = (int)(idx / N), n = (int)(idx - (size_t)m * N);
-  float acc = 0.f;
-  for (int kp = 0; kp < K / 2; ++kp) {
-    const uint32_t byte = B[code_offset<LAYOUT>(kp, n, K, N)];
-    const uint32_t sbyte = S[scale_offset<LAYOUT>(kp / 16, n, K, N)];
-    const uint32_t w = fp4x2_to_bf16x2<0>(byte, e8m0_to_f32(sbyte));
-    const float a0 = __builtin_bit_cast(float, (uint32_t)A[(size_t)m * K + 2 * kp] << 16);
-    const float a1 = __builtin_bit_cast(float, (uint32_t)A[(size_t)m * K + 2 * kp + 1] << 16);
-    acc = __builtin_fmaf(a0, __builtin_bit_cast(float, w << 16), acc);
-    acc = __builtin_fmaf(a1, __builtin_bit_cast(float, w & 0xFFFF0000u), acc);
+  const size_t total = (size_t)M * N;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const int m = (int)(idx / N), n = (int)(idx - (size_t)m * N);
+    float acc = 0.f;
+    for (int kp = 0; kp < K / 2; ++kp) {
+      const uint32_t byte = B[code_offset<LAYOUT>(kp, n, K, N)];
+      const uint32_t sbyte = S[scale_offset<LAYOUT>(kp / 16, n, K, N)];
+      const uint32_t w = fp4x2_to_bf16x2<0>(byte, e8m0_to_f32(sbyte));
+      const float a0 = __builtin_bit_cast(float, (uint32_t)A[(size_t)m * K + 2 * kp] << 16);
+      const float a1 = __builtin_bit_cast(float, (uint32_t)A[(size_t)m * K + 2 * kp + 1] << 16);
+      acc = __builtin_fmaf(a0, __builtin_bit_cast(float, w << 16), acc);
+      acc = __builtin_fmaf(a1, __builtin_bit_cast(float, w & 0xFFFF0000u), acc);
+    }
+    if (ep.any) acc = epilogue_value(ep, acc, m, n, N);
+    if (out_bf16)
+      static_cast<uint16_t*>(C)[idx] = (uint16_t)bf16_bits_rne(acc);
+    else
+      static_cast<float*>(C)[idx] = acc;
   }
-  if (ep.any) acc = epilogue_value(ep, acc, m, n, N);
-  if (out_bf16)
-    static_cast<uint16_t*>(C)[idx] = (uint16_t)bf16_bits_rne(acc);
-  else
-    static_cast<float*>(C)[idx] = acc;
 }
 
 // Layout conversion of the codes: one thread per 16 destination bytes (one
@@ -74,40 +96,41 @@ __global__ void __launch_bounds__(256) convert_codes_kernel(const uint8_t* __res
                                                             uint8_t* __restrict__ out, size_t K,
                                                             size_t N) {
   const size_t total = K / 2 * N;
-  const size_t o = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
-  if (o >= total) return;
-  size_t kp0, n0;
-  code_position<DST>(o, K, N, kp0, n0);
-  constexpr bool kRun = DST == kLayoutNK || DST == kLayoutP;  // 16 consecutive kp of one column
-  if constexpr (kRun && (SRC == kLayoutNK || SRC == kLayoutP)) {
-    *reinterpret_cast<u32x4*>(out + o) =
-        *reinterpret_cast<const u32x4*>(B + code_offset<SRC>(kp0, n0, K, N));
-    return;
-  }
-  uint8_t v[16];
-  const bool kn_row = DST == kLayoutKN && N % 16 == 0;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    size_t kp = kp0, n = n0;
-    if constexpr (kRun) {
-      kp = kp0 + i;
-    } else if constexpr (DST == kLayoutG) {
-      kp = kp0 + i % 4;
-      n = n0 + i / 4;
-    } else {
-      if (kn_row)
-        n = n0 + i;
-      else
-        code_position<DST>(o + i, K, N, kp, n);
+  for (size_t o = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16; o < total;
+       o += (size_t)gridDim.x * blockDim.x * 16) {
+    size_t kp0, n0;
+    code_position<DST>(o, K, N, kp0, n0);
+    constexpr bool kRun = DST == kLayoutNK || DST == kLayoutP;  // 16 consecutive kp of one column
+    if constexpr (kRun && (SRC == kLayoutNK || SRC == kLayoutP)) {
+      *reinterpret_cast<u32x4*>(out + o) =
+          *reinterpret_cast<const u32x4*>(B + code_offset<SRC>(kp0, n0, K, N));
+      continue;
     }
-    v[i] = B[code_offset<SRC>(kp, n, K, N)];
-  }
-  u32x4 w;
+    uint8_t v[16];
+    const bool kn_row = DST == kLayoutKN && N % 16 == 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    w[j] = (uint32_t)v[4 * j] | ((uint32_t)v[4 * j + 1] << 8) | ((uint32_t)v[4 * j + 2] << 16) |
-           ((uint32_t)v[4 * j + 3] << 24);
-  *reinterpret_cast<u32x4*>(out + o) = w;
+    for (int i = 0; i < 16; ++i) {
+      size_t kp = kp0, n = n0;
+      if constexpr (kRun) {
+        kp = kp0 + i;
+      } else if constexpr (DST == kLayoutG) {
+        kp = kp0 + i % 4;
+        n = n0 + i / 4;
+      } else {
+        if (kn_row)
+          n = n0 + i;
+        else
+          code_position<DST>(o + i, K, N, kp, n);
+      }
+      v[i] = B[code_offset<SRC>(kp, n, K, N)];
+    }
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = (uint32_t)v[4 * j] | ((uint32_t)v[4 * j + 1] << 8) | ((uint32_t)v[4 * j + 2] << 16) |
+             ((uint32_t)v[4 * j + 3] << 24);
+    *reinterpret_cast<u32x4*>(out + o) = w;
+  }
 }
 
 // Layout conversion of the scales: one thread per destination byte.
@@ -115,22 +138,25 @@ template <int SRC, int DST>
 __global__ void __launch_bounds__(256) convert_scales_kernel(const uint8_t* __restrict__ S,
                                                              uint8_t* __restrict__ out, size_t K,
                                                              size_t N) {
-  const size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (o >= K / 32 * N) return;
-  size_t g, n;
-  scale_position<DST>(o, K, N, g, n);
-  out[o] = S[scale_offset<SRC>(g, n, K, N)];
+  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < K / 32 * N;
+       o += (size_t)gridDim.x * blockDim.x) {
+    size_t g, n;
+    scale_position<DST>(o, K, N, g, n);
+    out[o] = S[scale_offset<SRC>(g, n, K, N)];
+  }
 }
 
 // 16 bytes per thread; vector stores when p is 16-byte aligned (C may be a
 // view at any element offset), byte stores otherwise and for the tail.
 __global__ void __launch_bounds__(256) zero_fill_kernel(uint8_t* p, size_t bytes) {
-  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
-  if (i + 16 <= bytes && ((uintptr_t)p & 15u) == 0) {
-    *reinterpret_cast<u32x4*>(p + i) = u32x4{0u, 0u, 0u, 0u};
-  } else {
-    const size_t end = i + 16 < bytes ? i + 16 : bytes;
-    for (size_t j = i; j < end; ++j) p[j] = 0;
+  for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16; i < bytes;
+       i += (size_t)gridDim.x * blockDim.x * 16) {
+    if (i + 16 <= bytes && ((uintptr_t)p & 15u) == 0) {
+      *reinterpret_cast<u32x4*>(p + i) = u32x4{0u, 0u, 0u, 0u};
+    } else {
+      const size_t end = i + 16 < bytes ? i + 16 : bytes;
+      for (size_t j = i; j < end; ++j) p[j] = 0;
+    }
   }
 }
 
@@ -154,7 +180,7 @@ struct DequantLaunch {
   static hipError_t run(const uint8_t* B, const uint8_t* S, void* out, int out_bf16, int K, int N,
                         hipStream_t stream) {
     const size_t total = (size_t)(K / 2) * N;
-    hipLaunchKernelGGL(dequant_kernel<L>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(dequant_kernel<L>, dim3(grid_for(total)), dim3(256), 0, stream,
                        B, S, out, out_bf16, K, N);
     return hipGetLastError();
   }
@@ -165,7 +191,7 @@ struct GenericLaunch {
   static hipError_t run(const uint16_t* A, const uint8_t* B, const uint8_t* S, void* C, int out_bf16,
                         int M, int N, int K, Epilogue ep, hipStream_t stream) {
     const size_t total = (size_t)M * N;
-    hipLaunchKernelGGL(generic_kernel<L>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(generic_kernel<L>, dim3(grid_for(total)), dim3(256), 0, stream,
                        A, B, S, C, out_bf16, M, N, K, ep);
     return hipGetLastError();
   }
@@ -178,11 +204,11 @@ struct ConvertFrom {
     static hipError_t run(const uint8_t* B, const uint8_t* S, uint8_t* B_out, uint8_t* S_out,
                           size_t K, size_t N, hipStream_t stream) {
       const size_t vecs = K / 2 * N / 16, sbytes = K / 32 * N;
-      hipLaunchKernelGGL((convert_codes_kernel<SRC, DST>), dim3((unsigned)((vecs + 255) / 256)),
+      hipLaunchKernelGGL((convert_codes_kernel<SRC, DST>), dim3(grid_for(vecs)),
                          dim3(256), 0, stream, B, B_out, K, N);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
-      hipLaunchKernelGGL((convert_scales_kernel<SRC, DST>), dim3((unsigned)((sbytes + 255) / 256)),
+      hipLaunchKernelGGL((convert_scales_kernel<SRC, DST>), dim3(grid_for(sbytes)),
                          dim3(256), 0, stream, S, S_out, K, N);
       return hipGetLastError();
     }
@@ -221,7 +247,7 @@ hipError_t launch_convert(int src_layout, int dst_layout, const uint8_t* B, cons
 hipError_t launch_zero_fill(void* C, size_t bytes, hipStream_t stream) {
   if (bytes == 0) return hipSuccess;
   const size_t chunks = (bytes + 15) / 16;
-  hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream,
+  hipLaunchKernelGGL(zero_fill_kernel, dim3(grid_for(chunks)), dim3(256), 0, stream,
                      static_cast<uint8_t*>(C), bytes);
   return hipGetLastError();
 }

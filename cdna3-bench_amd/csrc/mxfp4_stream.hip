@@ -422,15 +422,16 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
   // Reduction by the last arriver (only when a late unit gave up polling):
   // the same order as the late unit's fast path -- the other splits in
   // split order, then the late split.
+  // A poll that never completes (it cannot: every arrival follows its
+  // packet stores) writes NaN rather than a partial sum.
   auto reduce_from_packets = [&](int g) __attribute__((always_inline)) {
     const int rl = late_split(g);
     f32x4 tot[NV], own[NV];
-    sum_packets(g, rl, -1, tot);
-    f32x4 dummy[NV];
-    (void)dummy;
+    bool ok_all = sum_packets(g, rl, -1, tot);
     {
       u32x4 x0[NV], x1[NV];
-      for (int it = 0;; ++it) {
+      bool landed = false;
+      for (int it = 0; it <= (1 << 20); ++it) {
         bool ok = true;
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
@@ -438,14 +439,20 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
           x1[v] = load_packets(pr, packet_off(g, rl, v) + 16);
           ok = ok && tagged(x0[v], x1[v]);
         }
-        if (__builtin_amdgcn_ballot_w64(ok) == ~0ull || it > (1 << 20)) break;
+        if (__builtin_amdgcn_ballot_w64(ok) == ~0ull) {
+          landed = true;
+          break;
+        }
         __builtin_amdgcn_s_sleep(1);
       }
+      ok_all = ok_all && landed;
 #pragma unroll
       for (int v = 0; v < NV; ++v) own[v] = packet_values(x0[v], x1[v]);
     }
+    const float nan = __builtin_nanf("");
 #pragma unroll
-    for (int v = 0; v < NV; ++v) store_c(g, v, S > 1 ? tot[v] + own[v] : own[v]);
+    for (int v = 0; v < NV; ++v)
+      store_c(g, v, !ok_all ? f32x4{nan, nan, nan, nan} : S > 1 ? tot[v] + own[v] : own[v]);
     for (int rs = 0; rs < S; ++rs) clear_packets(g, rs);
     if (lane == 0) __hip_atomic_store(cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };

@@ -127,17 +127,9 @@ __global__ void __launch_bounds__(WM* WN * 64, 1) tiled_pipe_kernel(TiledArgs p)
   const int wm = wave / WN, wn = wave % WN;
   const int c = lane & 31, h = lane >> 5;
 
-  const int total = p.tiles_m * p.tiles_n * p.splits;
-  const int logical = xcd_chunked_id((int)blockIdx.x, total);
-  const int tile = logical / p.splits;
-  const int split = logical - tile * p.splits;
-  const int group_size = p.group_m * p.tiles_n;
-  const int group = tile / group_size;
-  const int first_m = group * p.group_m;
-  const int gm_rows = min(p.tiles_m - first_m, p.group_m);
-  const int in_group = tile - group * group_size;
-  const int tm = first_m + in_group % gm_rows;
-  const int tn = in_group / gm_rows;
+  const TileCoord tc = tile_of((int)blockIdx.x, p.tiles_m, p.tiles_n, p.splits, p.group_m);
+  const int tile = tc.tm * p.tiles_n + tc.tn;
+  const int split = tc.split, tm = tc.tm, tn = tc.tn;
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int M = p.M, N = p.N, K = p.K;

@@ -11,6 +11,8 @@ Reference functions and their counterparts:
   gemm_g            (kernels.py:59-60)  prepacked (strategy G) layout, read directly
   gemm_auto         (kernels.py:63-74)  every shape with K % 32 == 0
   device_info, shape_supported_{c,d,e,f,g} (kernels.py:11-32)
+  prepack_b_mxfp4   (kernels.py:8, re-exported from ref.py:85-101) the
+                    device prepack into the strategy-G arrays
 Additions: ``gemm`` (any weight layout, bf16/fp32 out, explicit plan),
 ``dequantize`` (device dequant tile), ``quantize`` (device quantize_mxfp4,
 ref.py:14-47), ``prepack`` / ``convert_layout``
@@ -27,12 +29,15 @@ except ImportError as e:  # pragma: no cover - exercised only without a build
         "mxfp4_cdna3._C not built; run `python cdna3-bench_amd/build.py`"
     ) from e
 
+from .ref import prepack_b_mxfp4  # noqa: F401,E402  (kernels.py:8 of the reference)
+
 LAYOUT_KN = "kn"  # B [K/2, N], S [K/32, N]  (reference API layout)
 LAYOUT_NK = "nk"  # B [N, K/2], S [N, K/32]  (K-contiguous weights)
 LAYOUT_G = "g"    # B [N/128, K/8, 128, 4], S [N/128, K/32, 128]  (strategy G prepack, N % 128 == 0)
 LAYOUT_P = "p"    # B [N/32, K/64, 2, 32, 16], S [N/32, K/64, 2, 32]  (panels, N % 32 == 0, K % 64 == 0)
 
 KERNEL_AUTO, KERNEL_GEMV, KERNEL_TILED, KERNEL_GENERIC, KERNEL_STREAM = 0, 1, 2, 3, 4
+PLAN_STREAM_NO_POLL = 1  # plan flag (tests): streaming split-K groups reduced by their last arrival
 
 
 def device_info(dev_id=0):
@@ -118,7 +123,10 @@ def gemm(A, B, S, C=None, layout=LAYOUT_KN, out_dtype=None, plan=None, bias=None
     any shape of the layout's size, N = B.numel() / (K/2)).
 
     out_dtype: torch.float32 (default) or torch.bfloat16 when C is None.
-    plan: optional (kernel, variant, split_k) overriding the cost model.
+    plan: optional (kernel, variant, split_k[, flags]) overriding the cost
+    model (flags: include/mxfp4_mi355x.h MXFP4_PLAN_*).
+    Split-K plans use a workspace the extension keeps per (device, stream);
+    under HIP graph capture, run the call once on the capturing stream first.
     bias [N], residual [M, N] (fp32 or bf16; residual may be C itself) and
     activation (None, "silu", "gelu", "gelu_tanh") are fused into the
     kernel's store, in fp32 before the rounding to C's dtype.
@@ -164,6 +172,11 @@ def prepack(B_packed, B_scales, layout=LAYOUT_P):
 def select_plan(M, N, K, layout=LAYOUT_KN):
     """(kernel, variant, split_k, description) the cost model picks."""
     return _ext.select_plan(M, N, K, layout)
+
+
+def describe_plan(plan):
+    """Description of a (kernel, variant, split_k[, flags]) plan."""
+    return _ext.describe_plan(list(plan))
 
 
 def version():

@@ -64,8 +64,17 @@ typedef struct mxfp4_plan {
   int32_t kernel;  /* MXFP4_KERNEL_* */
   int32_t variant; /* family-specific tile id (see mxfp4_plan_describe) */
   int32_t split_k; /* >= 1 */
-  int32_t reserved;
+  int32_t flags;   /* 0, or MXFP4_PLAN_* bits below */
 } mxfp4_plan;
+
+/*
+ * Plan flag for tests of the streaming split-K protocol (MXFP4_KERNEL_STREAM
+ * with split_k > 1; ignored otherwise): the late unit of each column group
+ * does not poll its partners' partials, so every group is reduced by the
+ * last of its arrivals -- the path the kernel takes when a group's CTAs are
+ * not resident together.  Results are bit-identical to the default path.
+ */
+#define MXFP4_PLAN_STREAM_NO_POLL 1
 
 /*
  * Fused epilogue: C = act(A x W + bias) + residual, in fp32, then rounded to
@@ -144,8 +153,10 @@ hipError_t mxfp4_gemm_ex(const void* A, const uint8_t* B, const uint8_t* S, void
 /*
  * out[K, N] = dequant(B, S) as bf16 (out_dtype MXFP4_OUT_BF16) or fp32.
  * Bit-exact device counterpart of dequantize_mxfp4(..., axis=0)
- * (python/mxfp4_cdna3/ref.py:50-72) for scale bytes 1..254; replaces
- * dequant_b_kernel (csrc/strategy_a_two_pass.cu:8-37).
+ * (python/mxfp4_cdna3/ref.py:50-72) for every scale byte: 0 scales by
+ * 2^-127 (subnormals kept), 255 gives +-inf and NaN for codes 0 and 8, as
+ * ref.py's float32 arithmetic does.  Replaces dequant_b_kernel
+ * (csrc/strategy_a_two_pass.cu:8-37).
  */
 hipError_t mxfp4_dequant(const uint8_t* B, const uint8_t* S, void* out, int out_dtype, int64_t K,
                          int64_t N, int b_layout, hipStream_t stream);

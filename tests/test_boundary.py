@@ -44,7 +44,7 @@ def lib():
 
 class Plan(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_int32), ("variant", ctypes.c_int32),
-                ("split_k", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("split_k", ctypes.c_int32), ("flags", ctypes.c_int32)]
 
 
 def test_header_symbols_exported(lib):
@@ -244,3 +244,22 @@ def test_scheduled_kernel_shape_rules(kk, lib, M, N, K, layout, sched):
     code = {"kn": 0, "nk": 1, "g": 2}[layout]
     ws = lib.mxfp4_gemm_workspace_bytes(M, N, K, code, ctypes.byref(Plan(2, 15, 2, 0)))
     assert (ws > 0) == sched, ws
+
+
+def test_stream_packets_must_fit_one_descriptor(lib):
+    """The streaming split-K packets are addressed through one 1 GiB buffer
+    descriptor: a P-layout decode shape with ~1.5 M columns would need more,
+    so no streaming plan is valid there and the selector picks another family."""
+    N, K = 1572864, 8192
+    for variant, split in ((4, 4), (2, 8)):  # the M <= 32 streaming shapes
+        assert lib.mxfp4_gemm_workspace_bytes(32, N, K, 3, ctypes.byref(Plan(4, variant, split, 0))) == 0
+    p, desc = _plan(lib, 32, N, K, 3)
+    assert p.kernel != 4, desc
+    p, desc = _plan(lib, 32, 8192, K, 3)
+    assert p.kernel == 4, desc  # the decode shape itself still streams
+
+
+def test_plan_flags_validated(lib):
+    ws = lib.mxfp4_gemm_workspace_bytes
+    assert ws(16, 8192, 8192, 1, ctypes.byref(Plan(4, 3, 2, 1))) > 0   # MXFP4_PLAN_STREAM_NO_POLL
+    assert ws(16, 8192, 8192, 1, ctypes.byref(Plan(4, 3, 2, 2))) == 0  # unknown flag bit

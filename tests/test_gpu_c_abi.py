@@ -1,0 +1,187 @@
+"""The C ABI on the GPU through ctypes, and the split-K workspace contract.
+
+* ``mxfp4_gemm`` called exactly as the ctypes binding in INTEGRATION.md shows
+  (zeroed workspace, the plumbing config), checked against the float64
+  oracle; the counters are zero again after the call.
+* The streaming split-K kernel's counter path (MXFP4_PLAN_STREAM_NO_POLL: no
+  late unit polls, every group is reduced by its last arrival) gives the
+  same bits as the default path and leaves counters and packets at zero.
+* Split-K calls alternating over two streams (the extension keeps one
+  workspace per stream) match the single-stream result.
+* HIP graph capture: a split-K call on a stream without a workspace is
+  refused before anything is recorded; after one eager call on that stream,
+  the captured graph replays the eager result, replay after replay.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from oracle import mxfp4_oracle as mo
+from tests.gpu_util import log, oracle_f64, to_dev_bf16, to_dev_u8, weights_for_layout
+
+pytestmark = pytest.mark.gpu
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(REPO, "cdna3-bench_amd", "mxfp4_cdna3", "libmxfp4_mi355x.so")
+LAYOUT = {"kn": 0, "nk": 1, "g": 2, "p": 3}
+COUNTER_BYTES = 1 << 20
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_int32), ("variant", ctypes.c_int32),
+                ("split_k", ctypes.c_int32), ("flags", ctypes.c_int32)]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import torch
+
+    assert torch.cuda.is_available()
+    import mxfp4_cdna3.kernels  # noqa: F401  (loads the HIP runtime the library links)
+
+    L = ctypes.CDLL(LIB)
+    i64, p = ctypes.c_int64, ctypes.c_void_p
+    # the binding of INTEGRATION.md
+    L.mxfp4_gemm.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] + [ctypes.c_int64] * 3 + \
+                            [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    L.mxfp4_gemm_with_plan.argtypes = [p, p, p, p, ctypes.c_int, i64, i64, i64, ctypes.c_int, p, p,
+                                       ctypes.c_size_t, p]
+    L.mxfp4_gemm_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int, p]
+    L.mxfp4_gemm_workspace_bytes.restype = ctypes.c_size_t
+    L.mxfp4_select_plan.argtypes = [i64, i64, i64, ctypes.c_int, p]
+    return L
+
+
+def _stream():
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def test_mxfp4_gemm_as_documented(lib):
+    import torch
+
+    M, N, K = 16, 2048, 2048  # the plumbing config
+    log(f"case ctypes mxfp4_gemm M={M} N={N} K={K}")
+    A_bits, W, S = mo.make_inputs(M, N, K, 122, 130, 1.0, seed=0)
+    Bkn, Skn = mo.nk_to_kn(W, S)
+    A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(Bkn), to_dev_u8(Skn)
+    ref = oracle_f64(A_bits, W, S)
+    wsb = lib.mxfp4_gemm_workspace_bytes(M, N, K, 0, None)
+    assert wsb > COUNTER_BYTES  # this plan splits K
+    ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")  # zero-filled once at allocation
+    outs = []
+    for c_dtype, dt in ((1, torch.bfloat16), (0, torch.float32), (1, torch.bfloat16)):
+        C = torch.empty(M, N, dtype=dt, device="cuda")
+        err = lib.mxfp4_gemm(A.data_ptr(), B.data_ptr(), Sd.data_ptr(), C.data_ptr(), c_dtype,
+                             M, N, K, 0, ws.data_ptr(), ws.numel(), _stream())
+        assert err == 0
+        torch.cuda.synchronize()
+        out = C.float().cpu().numpy()
+        assert mo.strict_violations(out, ref, K) == 0
+        assert ws[:COUNTER_BYTES].count_nonzero().item() == 0  # counters left at zero
+        outs.append(out)
+    assert np.array_equal(outs[0], outs[2])  # reused workspace: same bits
+    assert np.array_equal(outs[0], mo.bf16_bits_to_f32(mo.f32_to_bf16_bits(outs[1])))  # bf16 = RNE(fp32)
+    # a workspace that is too small is refused before anything runs
+    C = torch.empty(M, N, dtype=torch.float32, device="cuda")
+    assert lib.mxfp4_gemm(A.data_ptr(), B.data_ptr(), Sd.data_ptr(), C.data_ptr(), 0, M, N, K, 0,
+                          ws.data_ptr(), wsb - 1, _stream()) == 1
+
+
+@pytest.mark.parametrize("M,layout", [(16, "nk"), (16, "p"), (32, "nk"), (32, "p"), (12, "nk")])
+def test_stream_counter_path_matches_poll_path(lib, M, layout):
+    import torch
+
+    N, K = 8192, 8192
+    log(f"case stream split-K counter path M={M} layout={layout}")
+    A_bits, W, S = mo.make_inputs(M, N, K, 122, 130, 1.0, seed=M)
+    Bl, Sl = weights_for_layout(W, S, layout)
+    A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(Bl), to_dev_u8(Sl)
+    plan = Plan()
+    assert lib.mxfp4_select_plan(M, N, K, LAYOUT[layout], ctypes.byref(plan)) == 0
+    assert plan.kernel == 4 and plan.split_k > 1, "decode plan is the streaming split-K kernel"
+    wsb = lib.mxfp4_gemm_workspace_bytes(M, N, K, LAYOUT[layout], ctypes.byref(plan))
+    ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
+    outs = []
+    for flags in (0, 1, 0, 1):
+        plan.flags = flags
+        C = torch.empty(M, N, dtype=torch.float32, device="cuda")
+        err = lib.mxfp4_gemm_with_plan(A.data_ptr(), B.data_ptr(), Sd.data_ptr(), C.data_ptr(), 0,
+                                       M, N, K, LAYOUT[layout], ctypes.byref(plan), ws.data_ptr(), wsb,
+                                       _stream())
+        assert err == 0
+        torch.cuda.synchronize()
+        # counters and every packet are zero again
+        assert ws.count_nonzero().item() == 0, f"workspace not cleared (flags {flags})"
+        outs.append(C.cpu().numpy())
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    rows = np.arange(M)
+    cols = np.random.default_rng(0).choice(N, 512, replace=False)
+    ref = oracle_f64(A_bits, W, S, rows, cols)
+    assert mo.strict_violations(outs[1][:, cols], ref, K) == 0
+
+
+def test_split_k_on_two_streams(lib):
+    import torch
+
+    from mxfp4_cdna3 import kernels as kk
+
+    M, N, K = 16, 8192, 8192
+    log(f"case split-K on two streams M={M} N={N} K={K}")
+    A_bits, W, S = mo.make_inputs(M, N, K, 122, 130, 1.0, seed=11)
+    A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(W), to_dev_u8(S)
+    want = kk.gemm(A, B, Sd, None, "nk", torch.float32)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for i in range(8):
+        with torch.cuda.stream(streams[i % 2]):
+            outs.append(kk.gemm(A, B, Sd, None, "nk", torch.float32))
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o, want)
+
+
+def test_graph_capture_workspace(lib):
+    import torch
+
+    from mxfp4_cdna3 import kernels as kk
+
+    M, N, K = 16, 8192, 8192
+    log(f"case graph capture M={M} N={N} K={K}")
+    A_bits, W, S = mo.make_inputs(M, N, K, 122, 130, 1.0, seed=12)
+    A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(W), to_dev_u8(S)
+    assert kk.select_plan(M, N, K, "nk")[2] > 1  # split-K: needs a workspace
+    want = kk.gemm(A, B, Sd, None, "nk", torch.float32)
+    torch.cuda.synchronize()
+    C = torch.empty(M, N, dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="before the graph capture"):
+        with torch.cuda.graph(g, stream=s):
+            kk.gemm(A, B, Sd, C, "nk")
+    del g
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        kk.gemm(A, B, Sd, C, "nk")  # allocates this stream's workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        kk.gemm(A, B, Sd, C, "nk")
+    for _ in range(4):
+        C.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(C, want)
+        eager = kk.gemm(A, B, Sd, None, "nk", torch.float32)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(eager, want)

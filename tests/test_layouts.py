@@ -117,7 +117,7 @@ def test_device_index_functions_match_oracle(index_dump, layout, K, N):
 
 class Plan(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_int32), ("variant", ctypes.c_int32),
-                ("split_k", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("split_k", ctypes.c_int32), ("flags", ctypes.c_int32)]
 
 
 @pytest.fixture(scope="module")
