@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "mxfp4_kernels.h"
 #include "../../include/mxfp4_mi355x.h"
@@ -480,6 +481,53 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
 }  // namespace
 }  // namespace mxfp4
 
+// ---- the allocation-free entry point's workspace ------------------------------
+// One file-scope device array, loaded with this code object on every GPU the
+// library runs on (each GPU holds its own copy at its own address, until the
+// process ends): [split-K counters][partials], as the workspace of
+// mxfp4_gemm.  In host code `scratch` names a host-side stand-in, never the
+// device memory: the entry point uses the address hipGetSymbolAddress gives
+// for the current device.
+static __device__ __align__(256) uint8_t scratch[MXFP4_NOALLOC_SCRATCH_BYTES];
+
+namespace mxfp4 {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices];  // device address of `scratch`, per device
+
+// The current device's scratch, set up on the first call on that device:
+// its address, and one zero fill of the whole array (the counters and
+// split-K packets must start at zero; every call leaves them at zero), queued
+// on `stream` ahead of the call's kernels.  That fill has to run, not be
+// recorded: a first call on a device under stream capture is refused.
+hipError_t noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cap);
+    if (e != hipSuccess) return e;
+    if (cap != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (ptr == nullptr) return hipErrorInvalidSymbol;
+    e = launch_zero_fill(ptr, MXFP4_NOALLOC_SCRATCH_BYTES, stream);
+    if (e != hipSuccess) return e;
+    g_scratch[dev] = ptr;
+  }
+  *out = g_scratch[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+}  // namespace mxfp4
+
 using namespace mxfp4;
 
 extern "C" {
@@ -626,6 +674,18 @@ hipError_t mxfp4_device_info(int dev, mxfp4_device_info_t* out) {
   out->total_global_mem = (int64_t)prop.totalGlobalMem;
   out->shared_mem_per_block = (int64_t)prop.sharedMemPerBlock;
   return hipSuccess;
+}
+
+hipError_t mxfp4_gemm_noalloc(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype,
+                              int64_t M, int64_t N, int64_t K, int b_layout, hipStream_t stream) {
+  hipError_t e = check_args(A, B, S, C, c_dtype, M, N, K, b_layout);
+  if (e != hipSuccess) return e;
+  void* ws = nullptr;
+  e = noalloc_scratch(stream, &ws);
+  if (e != hipSuccess) return e;
+  const size_t need = mxfp4_gemm_workspace_bytes(M, N, K, b_layout, nullptr);
+  if (need > MXFP4_NOALLOC_SCRATCH_BYTES) return hipErrorOutOfMemory;
+  return run(A, B, S, C, c_dtype, M, N, K, b_layout, nullptr, nullptr, ws, MXFP4_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 const char* mxfp4_version(void) { return "mxfp4_mi355x 0.1.0 (gfx950)"; }

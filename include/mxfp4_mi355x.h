@@ -151,6 +151,26 @@ hipError_t mxfp4_gemm_ex(const void* A, const uint8_t* B, const uint8_t* S, void
                          hipStream_t stream);
 
 /*
+ * mxfp4_gemm without a workspace argument and without any allocation: the
+ * split-K workspace is a fixed device array of MXFP4_NOALLOC_SCRATCH_BYTES
+ * inside the library, one per GPU, held until the process ends (the first
+ * call on a GPU looks up its address and queues one zero fill of it on
+ * `stream`).  No counterpart in the reference: it is for callers that cannot
+ * allocate -- code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc.  Same plan, results and errors as mxfp4_gemm, plus
+ * hipErrorOutOfMemory when the plan's workspace (mxfp4_gemm_workspace_bytes)
+ * exceeds MXFP4_NOALLOC_SCRATCH_BYTES (nothing is launched then), and
+ * hipErrorStreamCaptureUnsupported when the first call on a GPU comes while
+ * `stream` is capturing a graph (that call's zero fill must run, not be
+ * recorded; later calls may be captured).  Every call
+ * on one GPU shares that GPU's array: calls that overlap in time on one GPU
+ * (other streams, other threads) race and must be ordered by the caller.
+ */
+#define MXFP4_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+hipError_t mxfp4_gemm_noalloc(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype,
+                              int64_t M, int64_t N, int64_t K, int b_layout, hipStream_t stream);
+
+/*
  * out[K, N] = dequant(B, S) as bf16 (out_dtype MXFP4_OUT_BF16) or fp32.
  * Bit-exact device counterpart of dequantize_mxfp4(..., axis=0)
  * (python/mxfp4_cdna3/ref.py:50-72) for every scale byte: 0 scales by

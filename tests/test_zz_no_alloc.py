@@ -1,0 +1,104 @@
+"""The allocation-free entry point ``mxfp4_gemm_noalloc`` through the C ABI.
+
+It runs the same auto plan as ``mxfp4_gemm`` with the library's own
+fixed-size device scratch in place of a caller workspace, so its output must
+be bit-identical to ``mxfp4_gemm``'s on the same inputs.  Two calls in a row
+(a split-K tiled plan, then a smaller streaming split-K plan) check that the
+scratch is left ready for the next call; a plan whose workspace exceeds the
+scratch is refused before anything runs.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from oracle import mxfp4_oracle as mo
+from tests.gpu_util import log, oracle_f64, to_dev_bf16, to_dev_u8, weights_for_layout
+
+pytestmark = pytest.mark.gpu
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(REPO, "cdna3-bench_amd", "mxfp4_cdna3", "libmxfp4_mi355x.so")
+LAYOUT = {"kn": 0, "nk": 1, "g": 2, "p": 3}
+SCRATCH_BYTES = 64 << 20  # MXFP4_NOALLOC_SCRATCH_BYTES
+HIP_ERROR_OUT_OF_MEMORY = 2
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import torch
+
+    assert torch.cuda.is_available()
+    import mxfp4_cdna3.kernels  # noqa: F401  (loads the HIP runtime the library links)
+
+    L = ctypes.CDLL(LIB)
+    i64, p = ctypes.c_int64, ctypes.c_void_p
+    L.mxfp4_gemm.argtypes = [p, p, p, p, ctypes.c_int, i64, i64, i64, ctypes.c_int, p, ctypes.c_size_t, p]
+    L.mxfp4_gemm_noalloc.argtypes = [p, p, p, p, ctypes.c_int, i64, i64, i64, ctypes.c_int, p]
+    L.mxfp4_gemm_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int, p]
+    L.mxfp4_gemm_workspace_bytes.restype = ctypes.c_size_t
+    return L
+
+
+def _stream():
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _inputs(M, N, K, layout, seed):
+    A_bits, W, S = mo.make_inputs(M, N, K, 122, 130, 1.0, seed=seed)
+    Bl, Sl = weights_for_layout(W, S, layout)
+    return A_bits, W, S, to_dev_bf16(A_bits), to_dev_u8(Bl), to_dev_u8(Sl)
+
+
+def test_noalloc_matches_mxfp4_gemm(lib):
+    import torch
+
+    # first a split-K tiled plan (about 29 MiB of partials), then a smaller
+    # streaming split-K plan: the second call reuses what the first left
+    cases = [(128, 28672, 8192, "kn", 1, 31), (16, 8192, 8192, "nk", 0, 32)]
+    for M, N, K, layout, c_dtype, seed in cases:
+        log(f"case mxfp4_gemm_noalloc M={M} N={N} K={K} layout={layout} c_dtype={c_dtype}")
+        wsb = lib.mxfp4_gemm_workspace_bytes(M, N, K, LAYOUT[layout], None)
+        assert 1 << 20 < wsb <= SCRATCH_BYTES, "the case must use split-K scratch and fit it"
+        A_bits, W, S, A, B, Sd = _inputs(M, N, K, layout, seed)
+        dt = torch.bfloat16 if c_dtype else torch.float32
+        ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
+        want = torch.empty(M, N, dtype=dt, device="cuda")
+        assert lib.mxfp4_gemm(A.data_ptr(), B.data_ptr(), Sd.data_ptr(), want.data_ptr(), c_dtype, M, N, K,
+                              LAYOUT[layout], ws.data_ptr(), wsb, _stream()) == 0
+        outs = []
+        for _ in range(2):
+            C = torch.full((M, N), float("nan"), dtype=dt, device="cuda")
+            assert lib.mxfp4_gemm_noalloc(A.data_ptr(), B.data_ptr(), Sd.data_ptr(), C.data_ptr(), c_dtype,
+                                          M, N, K, LAYOUT[layout], _stream()) == 0
+            torch.cuda.synchronize()
+            outs.append(C)
+        for C in outs:
+            assert torch.equal(C, want), "noalloc output differs from mxfp4_gemm"
+        rows = np.arange(min(M, 16))
+        cols = np.random.default_rng(seed).choice(N, 256, replace=False)
+        ref = oracle_f64(A_bits, W, S, rows, cols)
+        got = outs[0].float().cpu().numpy()[np.ix_(rows, cols)]
+        assert mo.strict_violations(got, ref, K) == 0
+
+
+def test_noalloc_refuses_plans_beyond_scratch(lib):
+    import torch
+
+    M, N, K = 64, 65536, 16384  # its auto plan needs 65 MiB of split-K workspace
+    assert lib.mxfp4_gemm_workspace_bytes(M, N, K, 0, None) > SCRATCH_BYTES
+    log(f"case mxfp4_gemm_noalloc refusal M={M} N={N} K={K}")
+    # real buffers of the full size, so nothing could be out of bounds
+    A = torch.zeros(M, K, dtype=torch.bfloat16, device="cuda")
+    B = torch.zeros(K // 2, N, dtype=torch.uint8, device="cuda")
+    S = torch.full((K // 32, N), 127, dtype=torch.uint8, device="cuda")
+    C = torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    err = lib.mxfp4_gemm_noalloc(A.data_ptr(), B.data_ptr(), S.data_ptr(), C.data_ptr(), 0, M, N, K, 0,
+                                 _stream())
+    torch.cuda.synchronize()
+    assert err == HIP_ERROR_OUT_OF_MEMORY
+    assert bool((C == 7.0).all()), "a refused call wrote C"
