@@ -89,6 +89,8 @@ const StreamShape kStream[] = {
     {2, 4, 2, 4, 4, 512},  // 4: M <= 32, split 2048 K (K <= 8192)
     {1, 16, 2, 1, 1, 512}, // 5: whole K, M <= 16, K <= 8192 (K / 512 waves)
     {1, 16, 2, 1, 1, 256}, // 6: whole K, M <= 16, K <= 4096 (K / 256 waves)
+    {1, 8, 4, 0, 8, 512, 16},  // 7: decode kernel, M <= 16, [N,K/2], 64 columns x 4096 K per CTA, K % 512 == 0
+    {1, 8, 2, 0, 8, 1024, 8},  // 8: decode kernel, M <= 8, [N,K/2], 32 columns x 8192 K per CTA, K % 1024 == 0
 };
 constexpr int kNumStream = sizeof(kStream) / sizeof(kStream[0]);
 constexpr int kStreamSpin = 4096;  // late-unit polls before counter arbitration
@@ -105,9 +107,11 @@ double problem_bytes(int64_t M, int64_t N, int64_t K, int c_bytes) {
 int64_t stream_splits(const StreamShape& s, int64_t K) { return ceil_div(K, s.k_split()); }
 int64_t stream_ctas(const StreamShape& s, int64_t N, int64_t K) {
   const int64_t splits = stream_splits(s, K);
+  if (s.direct) return ceil_div(N, 16 * s.gcb) * splits;
   return ceil_div(ceil_div(N, 32), splits) * splits;
 }
 bool stream_plan_ok(int layout, int64_t M, int64_t N, int64_t K, const StreamShape& s) {
+  if (s.direct) return decode_shape_ok(s.direct, layout, M, N, K);
   if ((layout != kLayoutNK && layout != kLayoutP) || M > 16 * s.mt || K % s.kw != 0) return false;
   const int64_t splits = stream_splits(s, K);
   if (splits > s.smax) return false;
@@ -155,9 +159,13 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
     // N = 8192 / 28672, K = 8192: whole-K 10.6 / 32.3 us at M = 1, 12.4 /
     // 40.7 us at M = 8, 15.8 / 52.7 us at M = 16; split-K 12.7 / 41.5 us at
     // M = 1, 13.1 / 42.7 us at M = 16).
-    static const int kPrefer8[] = {6, 5, 3, 0, 1}, kPrefer16[] = {3, 0, 1}, kPrefer32[] = {4, 2};
-    const int* pref = two ? kPrefer32 : M <= 8 ? kPrefer8 : kPrefer16;
-    const int npref = two ? 2 : M <= 8 ? 5 : 3;
+    // 2 <= M <= 8 with [N,K/2]: the decode kernel with the activations in LDS
+    // (variant 8) before those (M = 8: 11.8 / 39.4 us against 12.3 / 41.0 us
+    // whole-K; at M = 1 the whole-K kernel is faster, 10.4 against 11.1 us).
+    static const int kPrefer1[] = {6, 5, 3, 0, 1}, kPrefer8[] = {8, 6, 5, 3, 0, 1}, kPrefer16[] = {3, 0, 1},
+                     kPrefer32[] = {4, 2};
+    const int* pref = two ? kPrefer32 : M == 1 ? kPrefer1 : M <= 8 ? kPrefer8 : kPrefer16;
+    const int npref = two ? 2 : M == 1 ? 5 : M <= 8 ? 6 : 3;
     for (int i = 0; i < npref; ++i) {
       const StreamShape& st = kStream[pref[i]];
       if (stream_plan_ok(layout, M, N, K, st) && stream_ctas(st, N, K) >= 192) {
@@ -329,7 +337,7 @@ size_t plan_workspace(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_p
   } else if (p.kernel == MXFP4_KERNEL_STREAM) {
     const StreamShape& s = kStream[p.variant];
     // 8-byte (value, tag) packets per partial element
-    partial = (size_t)stream_ctas(s, N, K) * p.split_k * s.tile() * 8;
+    partial = s.direct ? decode_workspace(s.direct, N, K) : (size_t)stream_ctas(s, N, K) * p.split_k * s.tile() * 8;
   } else if (p.kernel == MXFP4_KERNEL_TILED) {
     const TiledShape& s = kTiled[p.variant].shape;
     const int64_t ksteps = ceil_div(K, 64);
@@ -554,7 +562,10 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
     case MXFP4_KERNEL_STREAM: {
       if (plan->variant < 0 || plan->variant >= kNumStream) return hipErrorInvalidValue;
       const StreamShape& s = kStream[plan->variant];
-      if (s.nslot == 1 && s.smax == 1)
+      if (s.direct)
+        snprintf(buf, buf_len, "decode rows%d cols%d kr%d split%d", s.direct, 16 * s.gcb, s.k_split(),
+                 plan->split_k);
+      else if (s.nslot == 1 && s.smax == 1)
         snprintf(buf, buf_len, "stream-whole mt%d kw%d split%d", s.mt, s.kw, plan->split_k);
       else
         snprintf(buf, buf_len, "stream mt%d w%d kw%d kr%d split%d", s.mt, s.waves, s.kw, s.k_split(),

@@ -1,0 +1,381 @@
+// Decode kernel for M <= 16 with [N, K/2] weights: activations resident in
+// LDS, weights streamed straight into VGPRs by separate waves.
+//
+// The reference has no kernel for these shapes (every launcher rejects
+// M % 64 != 0, csrc/common.h:80-99).  A decode GEMM is a read of the weights
+// (M = 16, N = K = 8192: 36.2 MB) plus 2 GFLOP of MFMA work, so its time is
+// set by how early and how many bytes the kernel puts in flight and by the
+// serial steps after the last byte lands.  Measured on MI355X (cold HBM:
+// buffers rotated past the 256 MB MALL; probes, not product code):
+//   - a bare 32-36 MB read takes 6.7-8.1 us per launch (about 1.6 us fixed);
+//     under that flood the first bytes land ~4 us after issue;
+//   - global loads are ~1.1 us faster than buffer loads of the same bytes,
+//     and the non-temporal hint helps global loads a little (it slows buffer
+//     loads);
+//   - activation loads in the MFMA operand layout (16 rows 2K bytes apart per
+//     instruction) cost 2.4x the same bytes read 1 KB-contiguous;
+//   - activation and weight loads issued by the same wave serialize (11.7 us
+//     for 64 MB of L2 activations + 32 MB of weights), while loader waves and
+//     weight waves overlap (9.5 us);
+//   - a CU's loads enter the memory system in issue order at the rate it
+//     accepts them (a wave that issues 16 loads at once is stalled in issue
+//     for up to 8 us), and every cross-CTA round trip at the end (publish,
+//     poll, store) adds ~1 us.
+//
+// So a CTA owns CW columns x KR of K with its activation slice (MR rows x KR,
+// 128 KB) resident in LDS:
+// * 8 loader waves DMA the activation slice (1 KB contiguous per DMA, 16-byte
+//   chunk j of row m landing at j ^ (m & 7): conflict-free operand reads;
+//   rows past M are skipped), then wait and release barrier B1.  The compute
+//   waves issue their loads only after the loaders have issued their DMAs
+//   (barrier B0): with the weights first, the activations landed after ~8 us,
+//   behind every weight byte of the CU.
+// * 8 compute waves each DMA their 1 KB scale block into LDS (an HBM read
+//   like the weights: in the loaders' queue it held B1 until the weight flood
+//   had drained), then keep 8 weight loads in flight -- CW columns x KR/8 of
+//   K in all, 16 bytes per lane (lane (c, q) reads bytes 64t + 16q .. +15 of
+//   its column's segment: 16 columns x 64 contiguous bytes per load), global
+//   non-temporal loads -- issuing the next as each lands and is consumed
+//   (waves that issued all 16 at once sat in issue until ~8 us).
+// * The K order inside one MFMA only has to agree between the operands:
+//   MFMA (t, s) of a 128-K step t takes K 128t + 32q + 8s .. +7 of the wave's
+//   range in lane (c, q): word s of the lane's 16 weight bytes and activation
+//   chunk 16t + 4q + s of row c.  Its scale is group 4t + q of the range.
+// * Each compute wave writes its partial tile into its own activation range
+//   (it alone reads that range), and the CTA sums the 8 tiles in wave order.
+// * Two shapes: MR = 8 (32 columns x the whole K up to 8192 per CTA: no
+//   split at K <= 8192) and MR = 16 (64 columns x 4096 K: 2 splits at K =
+//   8192).  Split CTAs publish their tile as tagged packets to the group's
+//   reducer (split S-1), which polls (bounded), adds the splits in split
+//   order, writes C, clears the packets and releases the group counter.  If
+//   the reducer gives up polling (CTAs not co-resident), it publishes too and
+//   the last of the S arrivals on the counter reduces.
+// * Out-of-range K ranges are DMAs past the descriptor's range (zeros land in
+//   LDS); columns past N load column N-1 and are zeroed.
+//
+// Result (N = K = 8192, bf16 C, graph-replayed): MR = 8 takes 11.8 us at
+// M = 8 against 12.3 us for the whole-K streaming kernel (N = 28672: 39.4
+// against 41.0 us), and is the auto plan for 2 <= M <= 8; at M = 1 the
+// streaming kernel is faster (10.4 against 11.1 us).  MR = 16 (15.4 us at
+// M = 16 against 12.7 us for the split-K streaming kernel) is an explicit
+// plan only: its 128 KB activation slice per CU queues ahead of the weights.
+#include "mxfp4_device.h"
+#include "mxfp4_kernels.h"
+
+namespace mxfp4 {
+namespace {
+
+template <int MR, int CW, int KR>
+struct DecodeCfg {
+  static constexpr int DEPTH = 8;                       // weight loads in flight per compute wave
+  static constexpr int CWAVES = 8;                      // compute waves
+  static constexpr int LWAVES = 8;                      // loader waves
+  static constexpr int NT = 64 * (CWAVES + LWAVES);
+  static constexpr int KWV = KR / CWAVES;               // K per compute wave
+  static constexpr int T = KWV / 128;                   // 128-K steps per compute wave
+  static constexpr int CB = CW / 16;                    // 16-column blocks
+  static constexpr int A_ROWB = 2 * KWV;                // activation bytes per row and range
+  static constexpr int A_RANGE = MR * A_ROWB;           // LDS bytes per compute wave's range
+  static constexpr int A_BYTES = CWAVES * A_RANGE;
+  static constexpr int A_DMAS = A_BYTES / 1024 / LWAVES;  // per loader wave
+  static constexpr int SW_COL = KWV / 32;               // scale bytes per column and compute wave
+  static constexpr int S_BYTES = CWAVES * 1024;         // one 1 KB scale block per compute wave
+  static constexpr int TILE = MR * CW;                  // outputs per CTA
+  static constexpr int ACTIVE = TILE / 4;               // threads holding 4 outputs
+  static constexpr int LDS = A_BYTES + S_BYTES;
+  static_assert(A_ROWB % 1024 == 0, "a 1 KB DMA covers part of one row");
+  static_assert(A_DMAS * LWAVES * 1024 == A_BYTES && A_DMAS < 48, "whole activation DMAs per loader wave");
+  static_assert(CW * SW_COL == 1024 && SW_COL % 16 == 0 && T * CB < 64, "one 1 KB scale DMA per compute wave");
+  static_assert(TILE * 4 <= A_RANGE && ACTIVE % 64 == 0 && ACTIVE <= 64 * CWAVES, "partial tiles");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+template <int MR, int CW, int KR>
+__global__ void __launch_bounds__(1024, 1) decode_kernel(StreamArgs p) {
+  using Cfg = DecodeCfg<MR, CW, KR>;
+  static_assert(Cfg::NT == 1024, "launch bounds");
+  constexpr int T = Cfg::T, CB = Cfg::CB, TILE = Cfg::TILE;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::LDS];
+  __shared__ int s_slow, s_last;
+  uint8_t* const alds = smem;
+  const uint8_t* const slds = smem + Cfg::A_BYTES;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int S = p.splits;
+  const int r = (int)blockIdx.x % S, g = (int)blockIdx.x / S;
+  const int M = p.M, N = p.N, K = p.K;
+  const int Kh = K >> 1, G = K >> 5;
+  const int kr0 = r * KR;
+  if (tid == 0) s_slow = 0;
+
+  f32x4 acc[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (wave >= Cfg::CWAVES) {
+    // ============================ loader wave ============================
+    const int lw = wave - Cfg::CWAVES;
+    const desc_t da = make_desc(p.A);
+#pragma unroll
+    for (int d = 0; d < Cfg::A_DMAS; ++d) {
+      const int D = lw * Cfg::A_DMAS + d;           // 1 KB block of the slice
+      const int cw = D / (Cfg::A_RANGE / 1024);     // compute wave's range
+      const int o = (D % (Cfg::A_RANGE / 1024)) * 1024;
+      const int m = o / Cfg::A_ROWB;
+      const int j = ((o % Cfg::A_ROWB) >> 4) + lane;  // LDS chunk position in the row
+      const int src = j ^ (m & 7);
+      const int k = kr0 + cw * Cfg::KWV;            // first K of the range
+      if (m >= M) continue;                         // rows past M are never read
+      dma16(da, alds + D * 1024, k < K ? (uint32_t)m * (uint32_t)K * 2u + 2u * (uint32_t)k + 16u * src : kOobOffset);
+    }
+    __builtin_amdgcn_s_barrier();  // B0: the activation DMAs are queued ahead of every weight load
+    wait_vmcnt0();
+    __builtin_amdgcn_s_barrier();  // B1: activations in LDS
+  } else {
+    // ============================ compute wave ===========================
+    const int c = lane & 15, q = lane >> 4;
+    const int cw = wave;
+    const int k0 = kr0 + cw * Cfg::KWV;  // K % KWV == 0: a range is all in or all out
+    const bool kok = k0 < K;
+    constexpr int NL = T * CB, D = Cfg::DEPTH < NL ? Cfg::DEPTH : NL;
+    u32x4 w[NL];
+    // weight load i = (t, cb) = (i / CB, i % CB): bytes 64t + 16q .. +15 of
+    // the range of column 16cb + c (columns past N read column N-1)
+    auto issue = [&](int i) __attribute__((always_inline)) {
+      const int t = i / CB, cb = i % CB;
+      const int n = CW * g + 16 * cb + c;
+      const int nc = n < N ? n : N - 1;
+      w[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(p.B + (size_t)nc * Kh + (k0 >> 1) + 64 * t + 16 * q));
+    };
+    __builtin_amdgcn_s_barrier();  // B0
+    __builtin_amdgcn_sched_barrier(0);
+    if (kok) {
+      // this wave's scale block (CW columns x KWV/32 groups = 1 KB) into its
+      // LDS slot, ahead of its weights: it lands first, with the first weights
+      const int byte = 16 * lane;
+      const int cl = byte / Cfg::SW_COL, gi = k0 / 32 + byte % Cfg::SW_COL;
+      const int n = CW * g + cl;
+      dma16(make_desc(p.S), slds + cw * 1024, n < N ? (uint32_t)n * (uint32_t)G + (uint32_t)gi : kOobOffset);
+#pragma unroll
+      for (int i = 0; i < D; ++i) issue(i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();  // B1 (the weights stay in flight)
+    __builtin_amdgcn_sched_barrier(0);
+    if (kok) {
+      // the scale DMA was issued before the D weight loads: it has landed once
+      // at most D are outstanding (an asm wait: the compiler does not see the
+      // DMA)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(D) : "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      bool nok[CB];
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) nok[cb] = CW * g + 16 * cb + c < N;
+      const bool rok = c < M;  // activation rows past M are not in LDS: zero operands
+      const uint8_t* const arow = alds + cw * Cfg::A_RANGE + (rok ? c : 0) * Cfg::A_ROWB;
+      const int swz = c & 7;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        u32x4 a[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          a[s] = rok ? *reinterpret_cast<const u32x4*>(arow + 16 * ((16 * t + 4 * q + s) ^ swz))
+                     : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const int i = t * CB + cb;
+          // groups 4t .. 4t+3 of the range for column 16cb + c; this lane's is byte q
+          const uint32_t sw = *reinterpret_cast<const uint32_t*>(slds + cw * 1024 + (16 * cb + c) * Cfg::SW_COL + 4 * t);
+          const float scale = e8m0_to_f32(sw >> (8 * q));
+          const u32x4 wv = nok[cb] ? w[i] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            acc[cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a[s]), operand_from_word(wv[s], scale), acc[cb]);
+          // keep D loads in flight: the next one is issued as this one is consumed
+          if (i + D < NL) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(i + D);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+    }
+    // the partial tile (rows 4q + i < MR, column 16cb + c) into this wave's
+    // own activation range, which no other wave reads
+    float* const part = reinterpret_cast<float*>(alds + cw * Cfg::A_RANGE);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * q + i < MR) part[(4 * q + i) * CW + 16 * cb + c] = acc[cb][i];
+  }
+  __syncthreads();  // B2: the partial tiles
+
+  // the CTA's sum in wave order: thread tid < ACTIVE owns elements 4 tid .. +3
+  const bool active = tid < Cfg::ACTIVE;
+  f32x4 own = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (active) {
+    own = *reinterpret_cast<const f32x4*>(alds + 16 * tid);
+#pragma unroll
+    for (int v = 1; v < Cfg::CWAVES; ++v) own += *reinterpret_cast<const f32x4*>(alds + v * Cfg::A_RANGE + 16 * tid);
+  }
+  const int row = tid / (CW / 4), col = CW * g + 4 * (tid % (CW / 4));
+  auto store_c = [&](f32x4 x) __attribute__((always_inline)) {
+    if (!active || row >= M) return;
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = p.ep.any ? epilogue_value(p.ep, x[i], row, col + i, N) : x[i];
+    if (p.out_bf16) {
+      uint16_t* out = static_cast<uint16_t*>(p.C) + (size_t)row * N + col;
+      if ((N & 3) == 0 && col + 3 < N) {
+        *reinterpret_cast<u32x2*>(out) = u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (col + i < N) out[i] = (uint16_t)bf16_bits_rne(y[i]);
+      }
+    } else {
+      float* out = static_cast<float*>(p.C) + (size_t)row * N + col;
+      if ((N & 3) == 0 && col + 3 < N) {
+        *reinterpret_cast<f32x4*>(out) = f32x4{y[0], y[1], y[2], y[3]};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (col + i < N) out[i] = y[i];
+      }
+    }
+  };
+  if (S == 1) {
+    store_c(own);
+    return;
+  }
+
+  // ---- split-K across the group's S CTAs ----
+  const __amdgpu_buffer_rsrc_t pr = make_rsrc(p.partials);
+  auto packet_off = [&](int rs_) __attribute__((always_inline)) {
+    return (uint32_t)((((size_t)g * S + rs_) * TILE + 4 * tid) * 8);
+  };
+  auto publish = [&]() __attribute__((always_inline)) {
+    if (active) store_packets(pr, packet_off(r), own, kTag);
+  };
+  auto clear = [&](int rs_) __attribute__((always_inline)) {
+    if (!active) return;
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, pr, packet_off(rs_), 0, kCPolDevice);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, pr, packet_off(rs_) + 16, 0, kCPolDevice);
+  };
+  // Split rs_'s packets of this thread, polled until tagged: at most `limit`
+  // rounds (limit < 0: 2^20 rounds, only for packets already published,
+  // whose stores are in flight).  Whole waves without outputs return at once.
+  auto poll = [&](int rs_, int limit, f32x4& val) __attribute__((always_inline)) -> bool {
+    if (tid >= Cfg::ACTIVE) {
+      val = f32x4{0.f, 0.f, 0.f, 0.f};
+      return true;
+    }
+    for (int it = 0;; ++it) {
+      const u32x4 x0 = load_packets(pr, packet_off(rs_)), x1 = load_packets(pr, packet_off(rs_) + 16);
+      if (__builtin_amdgcn_ballot_w64(tagged(x0, x1)) == __builtin_amdgcn_ballot_w64(true)) {
+        val = packet_values(x0, x1);
+        return true;
+      }
+      if (limit >= 0 ? it >= limit : it >= (1 << 20)) return false;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  };
+  // The last of the S arrivals: every split published; sum in split order
+  // (NaN instead of a partial sum if a published packet never showed up).
+  auto reduce_all = [&]() __attribute__((always_inline)) {
+    f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+    bool ok = true;
+    for (int rs_ = 0; rs_ < S; ++rs_) {
+      f32x4 v = own;
+      if (rs_ != r) ok = poll(rs_, -1, v) && ok;
+      tot = rs_ == 0 ? v : tot + v;
+    }
+    const float nan = __builtin_nanf("");
+    store_c(ok ? tot : f32x4{nan, nan, nan, nan});
+    for (int rs_ = 0; rs_ < S; ++rs_) clear(rs_);
+    if (tid == 0) __hip_atomic_store(p.counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  auto arrive_and_maybe_reduce = [&]() __attribute__((always_inline)) {
+    __syncthreads();  // every wave has issued its packet stores
+    if (tid == 0)
+      s_last = (int)((__hip_atomic_fetch_add(p.counters + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
+                      kArrivals) == (uint32_t)(S - 1));
+    __syncthreads();
+    if (s_last) reduce_all();
+  };
+
+  if (r != S - 1) {
+    publish();
+    arrive_and_maybe_reduce();
+    return;
+  }
+  // reducer: the other splits in split order, then its own
+  f32x4 others = f32x4{0.f, 0.f, 0.f, 0.f};
+  bool fast = true;
+  for (int rs_ = 0; rs_ < S - 1 && fast; ++rs_) {
+    f32x4 v;
+    fast = poll(rs_, p.spin_limit, v);
+    others = rs_ == 0 ? v : others + v;
+  }
+  if (!fast) s_slow = 1;
+  __syncthreads();
+  if (s_slow == 0) {
+    store_c(others + own);
+    for (int rs_ = 0; rs_ < S - 1; ++rs_) clear(rs_);
+    // The S - 1 arrivals and this subtraction net to zero in any order, and
+    // no arrival can see S - 1 arrivals before it (so none reduces).
+    if (tid == 0)
+      __hip_atomic_fetch_add(p.counters + g, (uint32_t)(1 - S), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  publish();
+  arrive_and_maybe_reduce();
+}
+
+using Dec16 = DecodeCfg<16, 64, 4096>;  // M <= 16: 64 columns x 4096 K per CTA
+using Dec8 = DecodeCfg<8, 32, 8192>;    // M <= 8: 32 columns x 8192 K per CTA
+
+}  // namespace
+
+int64_t decode_splits(int rows, int64_t K) {
+  const int64_t kr = rows <= 8 ? 8192 : 4096;
+  return (K + kr - 1) / kr;
+}
+int64_t decode_groups(int rows, int64_t N) {
+  const int64_t cw = rows <= 8 ? 32 : 64;
+  return (N + cw - 1) / cw;
+}
+size_t decode_workspace(int rows, int64_t N, int64_t K) {
+  const int64_t S = decode_splits(rows, K);
+  const int64_t tile = rows <= 8 ? 8 * 32 : 16 * 64;
+  return S > 1 ? (size_t)(decode_groups(rows, N) * S * tile * 8) : 0;
+}
+
+// Shape rules: M <= rows (8 or 16), K a multiple of one compute wave's range
+// (KR / 8: 1024 or 512 K), at most 8 splits, 32-bit offsets for activations,
+// scales and packets, one counter per column group.
+bool decode_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K) {
+  if (rows != 8 && rows != 16) return false;
+  const int64_t kwv = rows <= 8 ? 1024 : 512;
+  return layout == kLayoutNK && M >= 1 && M <= rows && K >= kwv && K % kwv == 0 && decode_splits(rows, K) <= 8 &&
+         M * K * 2 < (int64_t)kOobOffset && N * (K / 32) < (int64_t)kOobOffset &&
+         decode_workspace(rows, N, K) <= (size_t)kNumRecords && decode_groups(rows, N) * 4 <= (1 << 20);
+}
+
+hipError_t launch_decode(int rows, int layout, const StreamArgs& a, hipStream_t stream) {
+  if (!decode_shape_ok(rows, layout, a.M, a.N, a.K) || a.splits != decode_splits(rows, a.K))
+    return hipErrorInvalidValue;
+  if (a.splits > 1 && (!a.partials || !a.counters)) return hipErrorInvalidValue;
+  const unsigned grid = (unsigned)(decode_groups(rows, a.N) * a.splits);
+  if (rows <= 8)
+    hipLaunchKernelGGL((decode_kernel<8, 32, 8192>), dim3(grid), dim3(Dec8::NT), 0, stream, a);
+  else
+    hipLaunchKernelGGL((decode_kernel<16, 64, 4096>), dim3(grid), dim3(Dec16::NT), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace mxfp4

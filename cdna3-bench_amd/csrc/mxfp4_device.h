@@ -149,6 +149,17 @@ __device__ __forceinline__ void dma4(desc_t d, const void* lds, uint32_t voffset
   asm volatile("buffer_load_dword %0, %1, 0 offen lds"
                :: "v"(voffset), "s"(d), "{m0}"((uint32_t)(uintptr_t)lds) : "memory");
 }
+// The same with the non-temporal hint, for bytes read once per launch (the
+// decode kernels' weights and scales).  Measured on MI355X in a 36 MB decode
+// read: 1.2-1.4 us faster per launch than the same loads without it.
+__device__ __forceinline__ void dma16_nt(desc_t d, const void* lds, uint32_t voffset) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen nt lds"
+               :: "v"(voffset), "s"(d), "{m0}"((uint32_t)(uintptr_t)lds) : "memory");
+}
+__device__ __forceinline__ void dma4_nt(desc_t d, const void* lds, uint32_t voffset) {
+  asm volatile("buffer_load_dword %0, %1, 0 offen nt lds"
+               :: "v"(voffset), "s"(d), "{m0}"((uint32_t)(uintptr_t)lds) : "memory");
+}
 
 // Split-K partials cross XCDs, whose L2s are not coherent with each other.
 // Instead of __threadfence() (buffer_wbl2 + buffer_inv of the whole L2 on
@@ -212,6 +223,37 @@ __device__ __forceinline__ void splitk_sum(__amdgpu_buffer_rsrc_t rp, uint32_t s
 #pragma unroll
     for (int b = 0; b < GRP; ++b) put(g0 + b, sum[b]);
   }
+}
+
+// ---- split-K partials as tagged packets (streaming and decode kernels) ------
+// A published partial element is an 8-byte packet (value, tag), written with
+// device-coherent (SC1) stores and polled with SC1 loads, which see a packet
+// atomically; the reader needs no store-completion wait from the writer.
+// The tag is a quiet-NaN bit pattern with a rare payload, which no finite
+// partial that another split-K kernel leaves in the shared workspace can
+// equal (workspace words are zero or such partials).
+constexpr uint32_t kTag = 0x7FC5A3E1u;
+constexpr uint32_t kArrivals = 0xFFFFu;  // counter arrivals field (low half)
+
+// Whole vectors are bit-cast, never single components: hipcc's front end
+// lowers __builtin_bit_cast of a vector component (v.y) to a load from the
+// vector's first element.
+__device__ __forceinline__ void store_packets(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v, uint32_t tag) {
+  const u32x4 w = __builtin_bit_cast(u32x4, v);
+  const u32x4 lo = {w.x, tag, w.y, tag};
+  const u32x4 hi = {w.z, tag, w.w, tag};
+  __builtin_amdgcn_raw_buffer_store_b128(lo, r, off, 0, kCPolDevice);
+  __builtin_amdgcn_raw_buffer_store_b128(hi, r, off + 16, 0, kCPolDevice);
+}
+__device__ __forceinline__ u32x4 load_packets(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCPolDevice);
+}
+__device__ __forceinline__ bool tagged(u32x4 a, u32x4 b) {
+  return a.y == kTag && a.w == kTag && b.y == kTag && b.w == kTag;
+}
+__device__ __forceinline__ f32x4 packet_values(u32x4 a, u32x4 b) {
+  const f32x4 fa = __builtin_bit_cast(f32x4, a), fb = __builtin_bit_cast(f32x4, b);
+  return f32x4{fa.x, fa.z, fb.x, fb.z};
 }
 
 __device__ __forceinline__ uint32_t bf16_bits_rne(float f) {

@@ -58,15 +58,16 @@ struct GemvRegs<kLayoutNK, MT, CB> {
 };
 
 template <int N_>
+// Weight and scale words are read once per launch: non-temporal loads.
 __device__ __forceinline__ void load_words(uint32_t (&dst)[N_], const uint8_t* src, bool ok) {
   if constexpr (N_ == 4) {
-    u32x4 v = ok ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
+    u32x4 v = ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src)) : u32x4{0u, 0u, 0u, 0u};
     dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
   } else if constexpr (N_ == 2) {
-    u32x2 v = ok ? *reinterpret_cast<const u32x2*>(src) : u32x2{0u, 0u};
+    u32x2 v = ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src)) : u32x2{0u, 0u};
     dst[0] = v.x; dst[1] = v.y;
   } else {
-    dst[0] = ok ? *reinterpret_cast<const uint32_t*>(src) : 0u;
+    dst[0] = ok ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src)) : 0u;
   }
 }
 
@@ -125,9 +126,9 @@ __global__ void __launch_bounds__(WPC * 64, 1) gemv_kernel(GemvArgs p) {
       for (int cb = 0; cb < CB; ++cb) {
         const int col = n0 + cb * 16 + c;
         const bool ok = kok && col < N;
-        r.raw[cb] = ok ? *reinterpret_cast<const u32x4*>(p.B + (size_t)col * Kh + (k0 >> 1))
+        r.raw[cb] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.B + (size_t)col * Kh + (k0 >> 1)))
                        : u32x4{0u, 0u, 0u, 0u};
-        r.sb[cb] = ok ? (uint32_t)p.S[(size_t)col * G + (k0 >> 5)] : 0u;
+        r.sb[cb] = ok ? (uint32_t)__builtin_nontemporal_load(p.S + (size_t)col * G + (k0 >> 5)) : 0u;
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {

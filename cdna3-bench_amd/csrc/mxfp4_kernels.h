@@ -124,12 +124,23 @@ struct StreamShape {
   int nslot;  // LDS ring units per wave
   int smax;   // largest split count of this instantiation
   int kw;     // K per compute wave and unit (256 or 512)
+  int direct = 0;  // 8 or 16: the decode kernel (mxfp4_decode.hip) for M <= direct
   int k_split() const { return waves * kw; }
   int tile() const { return 16 * mt * 16 * gcb; }
 };
 
 hipError_t launch_stream(int layout, const StreamShape& shape, const StreamArgs& args, hipStream_t stream);
 bool stream_shape_available(const StreamShape& shape);
+
+// Decode kernel (mxfp4_decode.hip): [N,K/2], M <= rows with rows = 16 (64
+// columns x 4096 K per CTA) or 8 (32 columns x 8192 K per CTA), the CTA's
+// activation slice resident in LDS; S = ceil(K / KR) <= 8 CTAs per column
+// group, their tiles meeting as packets of decode_workspace bytes after the
+// counters.
+int64_t decode_splits(int rows, int64_t K);
+size_t decode_workspace(int rows, int64_t N, int64_t K);
+bool decode_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K);
+hipError_t launch_decode(int rows, int layout, const StreamArgs& args, hipStream_t stream);
 
 // Any shape with K % 32 == 0; one thread per output, for shapes the fast
 // families do not cover (N % 16 != 0, unaligned pointers).

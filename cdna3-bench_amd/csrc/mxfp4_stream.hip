@@ -42,12 +42,6 @@
 namespace mxfp4 {
 namespace {
 
-// Packet tag of a published partial: a quiet-NaN bit pattern with a rare
-// payload, which no finite partial that another split-K kernel leaves in the
-// shared workspace can equal (workspace words are zero or such partials).
-constexpr uint32_t kTag = 0x7FC5A3E1u;
-constexpr uint32_t kArrivals = 0xFFFFu;  // counter arrivals field (low half)
-
 template <int MT, int WAVES, int GCB, int NSLOT, int KW>
 struct StreamCfg {
   static_assert(KW == 256 || KW == 512, "K per wave and unit");
@@ -94,27 +88,6 @@ __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F
 template <int KW>
 __device__ __forceinline__ int chunk_rot(int i, int rr) {
   return KW == 256 ? (rr ^ i) : (4 * i + rr);
-}
-
-// Whole vectors are bit-cast, never single components: hipcc's front end
-// lowers __builtin_bit_cast of a vector component (v.y) to a load from the
-// vector's first element.
-__device__ __forceinline__ void store_packets(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v, uint32_t tag) {
-  const u32x4 w = __builtin_bit_cast(u32x4, v);
-  const u32x4 lo = {w.x, tag, w.y, tag};
-  const u32x4 hi = {w.z, tag, w.w, tag};
-  __builtin_amdgcn_raw_buffer_store_b128(lo, r, off, 0, kCPolDevice);
-  __builtin_amdgcn_raw_buffer_store_b128(hi, r, off + 16, 0, kCPolDevice);
-}
-__device__ __forceinline__ u32x4 load_packets(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCPolDevice);
-}
-__device__ __forceinline__ bool tagged(u32x4 a, u32x4 b) {
-  return a.y == kTag && a.w == kTag && b.y == kTag && b.w == kTag;
-}
-__device__ __forceinline__ f32x4 packet_values(u32x4 a, u32x4 b) {
-  const f32x4 fa = __builtin_bit_cast(f32x4, a), fb = __builtin_bit_cast(f32x4, b);
-  return f32x4{fa.x, fa.z, fb.x, fb.z};
 }
 
 template <int LAYOUT, int MT, int WAVES, int GCB, int NSLOT, int SMAX, int KW>
@@ -164,13 +137,13 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
         for (int k = 0; k < Cfg::SC_LOADS; ++k) {
           const int base = 256 * (Cfg::SC_LOADS * wave + k), byte = base + 4 * lane;
           const bool ok = live && r * Cfg::KR + 64 * (byte >> 6) < K;
-          dma4(ds, scr + sl * Cfg::SC_UNIT + base, ok ? (uint32_t)byte : kOobOffset);
+          dma4_nt(ds, scr + sl * Cfg::SC_UNIT + base, ok ? (uint32_t)byte : kOobOffset);
         }
         // weights: this wave's KW/64 consecutive 1 KB blocks of panel g
         const desc_t d = make_desc(p.B + ((size_t)g * (K / kPK) + (kw0 >> 6)) * 1024);
 #pragma unroll
         for (int i = 0; i < Cfg::W_LOADS; ++i)
-          dma16(d, wring + sl * SLOT + i * 1024, live && kok ? (uint32_t)(i * 1024 + 16 * lane) : kOobOffset);
+          dma16_nt(d, wring + sl * SLOT + i * 1024, live && kok ? (uint32_t)(i * 1024 + 16 * lane) : kOobOffset);
         return;
       }
       // scales: the unit's [GC][KR/32] block, wave w moving bytes
@@ -184,7 +157,7 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
           const int col = byte / Cfg::SC_COL, b = byte % Cfg::SC_COL;
           const int gi = r * Cfg::SC_COL + b;
           const bool ok = live && g * GC + col < N && gi < G;
-          dma4(d, scr + sl * Cfg::SC_UNIT + base, ok ? (uint32_t)(col * G + gi) : kOobOffset);
+          dma4_nt(d, scr + sl * Cfg::SC_UNIT + base, ok ? (uint32_t)(col * G + gi) : kOobOffset);
         }
       }
       const desc_t d = make_desc(p.B + (size_t)g * GC * Kh);
@@ -196,7 +169,7 @@ __global__ void __launch_bounds__((WAVES + 1) * 64, 1) stream_kernel(StreamArgs 
           const int col = 16 * cb + CPD * i + rr;
           const int j = ((lane % CH) - chunk_rot<KW>(i, rr)) & (CH - 1);
           const bool ok = live && kok && g * GC + col < N;
-          dma16(d, wring + sl * SLOT + (NI * cb + i) * 1024,
+          dma16_nt(d, wring + sl * SLOT + (NI * cb + i) * 1024,
                 ok ? (uint32_t)(col * Kh + (kw0 >> 1) + 16 * j) : kOobOffset);
         }
     };
@@ -626,13 +599,13 @@ __global__ void __launch_bounds__(1024, 1) stream_whole_kernel(StreamArgs p) {
     // contiguous in the panel
     const desc_t d = make_desc(p.B + ((size_t)g * (K / kPK) + (kw0 >> 6)) * 1024);
 #pragma unroll
-    for (int i = 0; i < Cfg::W_LOADS / 2; ++i) dma16(d, ws + i * 1024, (uint32_t)(i * 1024 + 16 * lane));
+    for (int i = 0; i < Cfg::W_LOADS / 2; ++i) dma16_nt(d, ws + i * 1024, (uint32_t)(i * 1024 + 16 * lane));
     const desc_t ds = make_desc(p.S + (size_t)g * (K / kPK) * 64 + kw0);
 #pragma unroll
-    for (int k = 0; k < Cfg::SC_LOADS; ++k) dma4(ds, ss + 256 * k, (uint32_t)(256 * k + 4 * lane));
+    for (int k = 0; k < Cfg::SC_LOADS; ++k) dma4_nt(ds, ss + 256 * k, (uint32_t)(256 * k + 4 * lane));
     issue_a();
 #pragma unroll
-    for (int i = Cfg::W_LOADS / 2; i < Cfg::W_LOADS; ++i) dma16(d, ws + i * 1024, (uint32_t)(i * 1024 + 16 * lane));
+    for (int i = Cfg::W_LOADS / 2; i < Cfg::W_LOADS; ++i) dma16_nt(d, ws + i * 1024, (uint32_t)(i * 1024 + 16 * lane));
   } else {
     // weights: DMA i of block cb moves CPD whole column segments (KW/2
     // bytes); chunk j of column 16cb + CPD*i + rr lands at 16-byte position
@@ -645,7 +618,7 @@ __global__ void __launch_bounds__(1024, 1) stream_whole_kernel(StreamArgs p) {
         const int col = 16 * cb + CPD * i + rr;
         const int j = ((lane % CH) - chunk_rot<KW>(i, rr)) & (CH - 1);
         const bool ok = g * 32 + col < N;
-        dma16(d, ws + (NI * cb + i) * 1024, ok ? (uint32_t)(col * Kh + (kw0 >> 1) + 16 * j) : kOobOffset);
+        dma16_nt(d, ws + (NI * cb + i) * 1024, ok ? (uint32_t)(col * Kh + (kw0 >> 1) + 16 * j) : kOobOffset);
       }
     };
     issue_w(0);
@@ -657,7 +630,7 @@ __global__ void __launch_bounds__(1024, 1) stream_whole_kernel(StreamArgs p) {
         const int byte = 256 * k + 4 * lane;
         const int col = byte / CH, b = byte % CH;
         const bool ok = g * 32 + col < N;
-        dma4(ds, ss + 256 * k, ok ? (uint32_t)(col * G + kw0 / 32 + b) : kOobOffset);
+        dma4_nt(ds, ss + 256 * k, ok ? (uint32_t)(col * G + kw0 / 32 + b) : kOobOffset);
       }
     }
     issue_a();
@@ -818,6 +791,9 @@ bool whole_shape(const StreamShape& s) {
 }
 
 bool stream_shape_available(const StreamShape& s) {
+  if (s.direct)
+    return s.mt == 1 && s.waves == 8 && s.nslot == 0 && s.smax == 8 &&
+           ((s.direct == 16 && s.gcb == 4 && s.kw == 512) || (s.direct == 8 && s.gcb == 2 && s.kw == 1024));
   if (whole_shape(s)) return true;
 #define X(MT_, W_, GCB_, NS_, SM_, KW_)                                                              \
   if (s.mt == MT_ && s.waves == W_ && s.gcb == GCB_ && s.nslot == NS_ && s.smax == SM_ && s.kw == KW_) \
@@ -828,6 +804,7 @@ bool stream_shape_available(const StreamShape& s) {
 }
 
 hipError_t launch_stream(int layout, const StreamShape& s, const StreamArgs& args, hipStream_t stream) {
+  if (s.direct) return launch_decode(s.direct, layout, args, stream);
   if (whole_shape(s)) {
     if (args.splits != 1) return hipErrorInvalidValue;
     return s.kw == 512 ? launch_whole<512>(layout, args, stream) : launch_whole<256>(layout, args, stream);

@@ -187,6 +187,10 @@ def test_plan_from_python(kk):
     kind, _, split, desc = kk.select_plan(16, 8192, 8192, "nk")
     assert kind == kk.KERNEL_STREAM and desc.startswith("stream ") and split == 2
     kind, _, split, desc = kk.select_plan(8, 8192, 8192, "nk")
+    assert kind == kk.KERNEL_STREAM and desc.startswith("decode rows8") and split == 1
+    kind, _, split, desc = kk.select_plan(1, 8192, 8192, "nk")
+    assert kind == kk.KERNEL_STREAM and desc.startswith("stream-whole") and split == 1
+    kind, _, split, desc = kk.select_plan(8, 8192, 8192, "p")
     assert kind == kk.KERNEL_STREAM and desc.startswith("stream-whole") and split == 1
     kind, _, _, desc = kk.select_plan(16, 8192, 8192, "kn")
     assert kind == kk.KERNEL_GEMV and desc.startswith("gemv")

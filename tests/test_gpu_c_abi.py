@@ -126,6 +126,41 @@ def test_stream_counter_path_matches_poll_path(lib, M, layout):
     assert mo.strict_violations(outs[1][:, cols], ref, K) == 0
 
 
+@pytest.mark.parametrize("variant,M,K", [(7, 16, 8192), (8, 8, 16384), (7, 13, 12800)])
+def test_decode_counter_path_matches_poll_path(lib, variant, M, K):
+    """The decode kernel's split-K protocol: the reducer's poll path (flags 0)
+    and the arrival-counter path (MXFP4_PLAN_STREAM_NO_POLL: the reducer
+    gives up at once and the last arrival reduces) give the same bits, and
+    leave counters and packets at zero."""
+    import torch
+
+    N = 4096
+    log(f"case decode split-K counter path variant={variant} M={M} K={K}")
+    A_bits, W, S = mo.make_inputs(M, N, K, 122, 130, 1.0, seed=variant + M)
+    A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(W), to_dev_u8(S)
+    kr = 4096 if variant == 7 else 8192
+    plan = Plan(4, variant, -(-K // kr), 0)
+    assert plan.split_k > 1
+    wsb = lib.mxfp4_gemm_workspace_bytes(M, N, K, LAYOUT["nk"], ctypes.byref(plan))
+    assert wsb > COUNTER_BYTES
+    ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
+    outs = []
+    for flags in (0, 1, 0, 1):
+        plan.flags = flags
+        C = torch.empty(M, N, dtype=torch.float32, device="cuda")
+        err = lib.mxfp4_gemm_with_plan(A.data_ptr(), B.data_ptr(), Sd.data_ptr(), C.data_ptr(), 0,
+                                       M, N, K, LAYOUT["nk"], ctypes.byref(plan), ws.data_ptr(), wsb, _stream())
+        assert err == 0
+        torch.cuda.synchronize()
+        assert ws.count_nonzero().item() == 0, f"workspace not cleared (flags {flags})"
+        outs.append(C.cpu().numpy())
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    cols = np.random.default_rng(1).choice(N, 256, replace=False)
+    ref = oracle_f64(A_bits, W, S, np.arange(M), cols)
+    assert mo.strict_violations(outs[1][:, cols], ref, K) == 0
+
+
 def test_split_k_on_two_streams(lib):
     import torch
 

@@ -333,6 +333,46 @@ def test_stream_whole_rejects(kk, variant, kw, kmax):
             run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=(kk.KERNEL_STREAM, variant, split))
 
 
+# decode kernel variants: (variant, rows, K per split, K granularity)
+DECODE_VARIANTS = [(7, 16, 4096, 512), (8, 8, 8192, 1024)]
+
+
+@pytest.mark.parametrize("variant,rows,kr,kg", DECODE_VARIANTS)
+def test_decode_variants(kk, variant, rows, kr, kg):
+    """Decode kernel ([N,K/2], M <= rows): one split, a partial last split,
+    up to 8 splits, ragged M, N % 64 != 0 and odd N (element stores), fp32
+    and bf16 out; repeat calls are bitwise identical and bf16 out is the
+    fp32 result rounded."""
+    import torch
+
+    for M in sorted({1, 7, rows}):
+        for N, K in ((512, kg), (1000, kr + kg), (1001, 2 * kg), (4096, 8192), (96, 8192), (200, 3 * kr),
+                     (256, 8 * kr)):
+            splits = -(-K // kr)
+            log(f"case decode variant={variant} M={M} N={N} K={K} splits={splits}")
+            A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=M + N + K + 11)
+            ref = oracle_f64(A_bits, W, S)
+            plan = (kk.KERNEL_STREAM, variant, splits)
+            out = run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan)
+            bad = mo.strict_violations(out, ref, K)
+            assert bad == 0, f"M={M} N={N} K={K}: {bad} bad"
+            again = run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan)
+            assert np.array_equal(out, again), f"M={M} N={N} K={K}: not deterministic"
+            out16 = run_gemm(kk, A_bits, W, S, "nk", torch.bfloat16, plan=plan)
+            assert np.array_equal(out16, mo.bf16_bits_to_f32(mo.f32_to_bf16_bits(out))), f"M={M} N={N} K={K}"
+
+
+@pytest.mark.parametrize("variant,rows,kr,kg", DECODE_VARIANTS)
+def test_decode_rejects(kk, variant, rows, kr, kg):
+    import torch
+
+    for M, K, layout, split in ((rows + 1, kg, "nk", 1), (rows, 8 * kr + kg, "nk", 9), (rows, kg + 256, "nk", 1),
+                                (rows, kg, "p", 1), (rows, kg, "kn", 1), (rows, 2 * kr, "nk", 1)):
+        A_bits, W, S = mo.make_inputs(M, 64, K, 120, 132, seed=4)
+        with pytest.raises(RuntimeError, match="invalid argument"):  # M, splits, K granularity, layout, split count
+            run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=(kk.KERNEL_STREAM, variant, split))
+
+
 @pytest.mark.parametrize("M", [24, 32])
 def test_wide_nk_decode_takes_gemv(kk, M):
     """[N,K/2], 16 < M <= 32, N >= 16384: the auto plan is the GEMV family
