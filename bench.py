@@ -34,9 +34,13 @@ flops and roofline columns, and times the CPU path per config.  The CSV
 feeds ``python -m mxfp4_cdna3.cost_model --fit <csv>`` (the reference's
 scripts/run_bench.sh:12-14 -> cost_model.py:153-167).
 
+--leg CONFIG:LAYOUT[:KIND,VARIANT,SPLIT] times one config in one layout (auto
+or explicit plan) and prints its record: the unit of the committed rocprofv3
+summaries (profiles/), one kernel per run.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout kn|nk|g]
                        [--no-cpu] [--no-decode] [--no-extra] [--calibrate-copy]
-                       [--sweep [--csv PATH]]
+                       [--sweep [--csv PATH]] [--leg CONFIG:LAYOUT[:PLAN]]
 """
 
 import argparse
@@ -442,6 +446,19 @@ def sweep(args, kk):
     return {"sweep": summary, "cpu_model": cpu_model(), "csv": args.csv}
 
 
+def single_leg(args, kk):
+    """One config in one layout: the record of a profiled run."""
+    parts = args.leg.split(":")
+    cfg = CONFIGS[parts[0]]
+    lay = parts[1] if len(parts) > 1 else "kn"
+    plan = tuple(int(x) for x in parts[2].split(",")) if len(parts) > 2 else None
+    steps = max(args.steps, 200) if cfg["M"] <= 32 else args.steps
+    rec = leg_record(cfg, measure(kk, cfg, lay, steps, args.warmup, args.warm_s, plan))
+    if args.calibrate_copy:
+        copy_calibration()
+    return {"leg": args.leg, "M": cfg["M"], "N": cfg["N"], "K": cfg["K"], "layout": lay, "steps": steps, **rec}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -458,6 +475,7 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="time every BASELINE config (CSV)")
     ap.add_argument("--csv", default=None, help="--sweep: CSV output path")
     ap.add_argument("--cpu-s", type=float, default=3.0, help="--sweep: CPU seconds per config")
+    ap.add_argument("--leg", default=None, help="one config: CONFIG:LAYOUT[:KIND,VARIANT,SPLIT]")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -472,7 +490,7 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.synchronize()
-    result = sweep(args, kk) if args.sweep else headline(args, kk)
+    result = single_leg(args, kk) if args.leg else sweep(args, kk) if args.sweep else headline(args, kk)
     print(json.dumps(result), flush=True)
 
 

@@ -132,6 +132,38 @@ def summarize(trace: str, kernel_re: str, pmc: list[str], copy_bytes: float | No
             busy = merged["SQ_VALU_MFMA_BUSY_CYCLES"] / (4.0 * merged["SQ_BUSY_CU_CYCLES"])
             result["mfma_busy"] = busy
             lines += ["", f"MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (4 x SQ_BUSY_CU_CYCLES) = {100*busy:.1f}%"]
+        # latency, occupancy and cache figures from the raw counters
+        derived = []
+        if "VmemLatency" in merged:
+            result["vmem_latency_cycles"] = merged["VmemLatency"]
+            derived.append(f"- vector memory latency (VmemLatency: accumulated SQ_INST_LEVEL_VMEM / SQ_INSTS_VMEM) = "
+                           f"{merged['VmemLatency']:.0f} cycles")
+        if "MeanOccupancyPerActiveCU" in merged:
+            result["waves_per_busy_cu"] = merged["MeanOccupancyPerActiveCU"]
+            derived.append(f"- resident waves per SIMD of a busy CU (MeanOccupancyPerActiveCU) = "
+                           f"{merged['MeanOccupancyPerActiveCU']:.2f}")
+        if "VmemLatency" not in merged and merged.get("SQ_INSTS_VMEM") and "SQ_INST_LEVEL_VMEM" in merged:
+            v = merged["SQ_INST_LEVEL_VMEM"] / merged["SQ_INSTS_VMEM"]
+            result["vmem_latency_cycles"] = v
+            derived.append(f"- vector memory latency = SQ_INST_LEVEL_VMEM / SQ_INSTS_VMEM = {v:.0f} cycles")
+        if "MeanOccupancyPerActiveCU" not in merged and merged.get("SQ_BUSY_CU_CYCLES") and "SQ_LEVEL_WAVES" in merged:
+            v = merged["SQ_LEVEL_WAVES"] / merged["SQ_BUSY_CU_CYCLES"]
+            result["waves_per_busy_cu"] = v
+            derived.append(f"- resident waves per busy CU = SQ_LEVEL_WAVES / SQ_BUSY_CU_CYCLES = {v:.2f}")
+        hit, miss = merged.get("TCC_HIT_sum", merged.get("TCC_HIT")), merged.get("TCC_MISS_sum", merged.get("TCC_MISS"))
+        if hit is not None and miss is not None and hit + miss > 0:
+            result["l2_hit"] = hit / (hit + miss)
+            derived.append(f"- L2 hit rate = TCC_HIT / (TCC_HIT + TCC_MISS) = {100 * hit / (hit + miss):.1f}%")
+        lvl = merged.get("TCC_EA0_RDREQ_LEVEL_sum", merged.get("TCC_EA0_RDREQ_LEVEL"))
+        req = merged.get("TCC_EA0_RDREQ_sum", merged.get("TCC_EA0_RDREQ"))
+        if lvl is not None and req:
+            result["ea_read_latency_cycles"] = lvl / req
+            derived.append(f"- L2-miss (EA) read latency = TCC_EA0_RDREQ_LEVEL / TCC_EA0_RDREQ = {lvl / req:.0f} cycles")
+        if merged.get("SQ_WAIT_INST_ANY") is not None and merged.get("SQ_WAVES"):
+            derived.append(f"- cycles a wave waited on any instruction dependency, per wave = "
+                           f"{merged['SQ_WAIT_INST_ANY'] / merged['SQ_WAVES']:.0f}")
+        if derived:
+            lines += ["", "## latency, occupancy, cache", ""] + derived
     if copy_bytes and copy_c and ("FETCH_SIZE" in merged or "WRITE_SIZE" in merged):
         lines += ["", f"## HBM traffic (copy calibration: {copy_bytes/2**20:.0f} MiB copy)", ""]
         traffic = 0.0
