@@ -179,21 +179,56 @@ def predict_all(shapes, hw: HwProfile = MI355X, strategies=STRATEGIES):
     return [predict(s, sh, hw) for sh in shapes for s in strategies]
 
 
-def fit_efficiency(bench_csv: str, hw: HwProfile = MI355X) -> dict[str, float]:
+def fit_efficiency(bench_csv: str, hw: HwProfile = MI355X, peak_tflops: float | None = None) -> dict[str, float]:
     """Invert measured times -> achievable_eff per strategy (median across
     shapes of peak time / measured time), as cost_model.py:153-167.  The CSV
-    has columns strategy, M, N, K, ns (one row per iteration or per shape)."""
+    has columns strategy, M, N, K, ns (one row per iteration or per shape).
+    ``peak_tflops`` overrides the hardware peak (the C++ selector's
+    efficiencies are fractions of 2500 TFLOP/s)."""
+    peak = peak_tflops if peak_tflops else hw.mfma_peak_tflops
+    per_strategy: dict[str, list[float]] = {}
+    for (strat, M, N, K), p50 in _p50_rows(bench_csv).items():
+        peak_ns = ProblemShape(M, N, K).flops / (peak * 1e12) * 1e9
+        per_strategy.setdefault(strat, []).append(peak_ns / p50)
+    return {s: float(sorted(v)[len(v) // 2]) for s, v in per_strategy.items()}
+
+
+def _p50_rows(bench_csv: str) -> dict[tuple, float]:
+    """{(strategy, M, N, K): median ns} of a bench CSV."""
     rows: dict[tuple, list[float]] = {}
     with open(bench_csv, newline="") as f:
         for r in csv.DictReader(f):
             key = (r["strategy"], int(r["M"]), int(r["N"]), int(r["K"]))
             rows.setdefault(key, []).append(float(r["ns"]))
-    per_strategy: dict[str, list[float]] = {}
-    for (strat, M, N, K), ns in rows.items():
-        p50 = sorted(ns)[len(ns) // 2]
-        peak_ns = ProblemShape(M, N, K).flops / (hw.mfma_peak_tflops * 1e12) * 1e9
-        per_strategy.setdefault(strat, []).append(peak_ns / p50)
-    return {s: float(sorted(v)[len(v) // 2]) for s, v in per_strategy.items()}
+    return {k: sorted(v)[len(v) // 2] for k, v in rows.items()}
+
+
+def write_sweep_summary(bench_csv: str, path: str, command: str = "", peak_tflops: float = 2500.0):
+    """Markdown summary of a ``bench.py --sweep`` CSV: every (config, strategy)
+    with its plan, median time and roofline fraction, then the efficiencies
+    fitted for the selector's tiled variants (fractions of ``peak_tflops``)."""
+    plans, fracs = {}, {}
+    with open(bench_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            key = (r["strategy"], int(r["M"]), int(r["N"]), int(r["K"]))
+            plans[key] = r.get("plan", "")
+            fracs[key] = (r.get("bound", ""), r.get("frac", ""))
+    p50 = _p50_rows(bench_csv)
+    lines = ["# Sweep of the BASELINE configs (bench.py --sweep)", ""]
+    if command:
+        lines += [f"command: `{command}`", ""]
+    lines += ["| M | N | K | strategy | plan | median us | bound | roofline frac |", "|---|---|---|---|---|---|---|---|"]
+    for (strat, M, N, K), ns in sorted(p50.items(), key=lambda kv: (kv[0][1], kv[0][2], kv[0][3], kv[0][0])):
+        bound, frac = fracs[(strat, M, N, K)]
+        us = f"{ns / 1e3:.3f}" if strat != "cpu-torch-fp32" else f"{ns / 1e3:.1f}"
+        lines.append(f"| {M} | {N} | {K} | {strat} | {plans[(strat, M, N, K)]} | {us} | {bound} | {frac} |")
+    fit = fit_efficiency(bench_csv, peak_tflops=peak_tflops)
+    lines += ["", f"## fitted efficiencies (median over the MFMA-bound configs of peak time / measured time, "
+                  f"peak {peak_tflops:.0f} TFLOP/s)", "", "| strategy | efficiency |", "|---|---|"]
+    for st in sorted(k for k in fit if k.startswith("tiled-v")):
+        lines.append(f"| {st} | {fit[st]:.3f} |")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
 
 
 def write_predictions_csv(rows: list[Prediction], path: str):
@@ -226,10 +261,15 @@ def main(argv=None):
     ap = argparse.ArgumentParser(description="MI355X roofline predictions for the MXFP4 GEMM")
     ap.add_argument("--out", default=None, help="write predictions as CSV")
     ap.add_argument("--fit", default=None, help="bench CSV (strategy,M,N,K,ns) to fit efficiencies")
+    ap.add_argument("--peak", type=float, default=None, help="--fit: peak TFLOP/s (default: the hardware's)")
+    ap.add_argument("--summary", default=None, help="--fit: write a markdown summary of the CSV here")
+    ap.add_argument("--command", default="", help="--summary: the command that produced the CSV")
     a = ap.parse_args(argv)
     if a.fit:
-        for s, e in sorted(fit_efficiency(a.fit).items()):
+        for s, e in sorted(fit_efficiency(a.fit, peak_tflops=a.peak).items()):
             print(f"{s}: achievable_eff = {e:.3f}")
+        if a.summary:
+            write_sweep_summary(a.fit, a.summary, a.command, a.peak or 2500.0)
         return
     rows = predict_all(BASELINE_SHAPES)
     for r in rows:

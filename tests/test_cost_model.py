@@ -91,3 +91,26 @@ def test_predictions_csv(tmp_path):
     with open(out) as f:
         got = list(csv.DictReader(f))
     assert len(got) == len(rows) and {"M", "N", "K", "binding", "predicted_ns"} <= set(got[0])
+
+
+def test_selector_efficiencies_are_the_committed_sweep_fit():
+    """The C++ selector's efficiencies of the re-measured tiled variants (6, 7,
+    15) are the fit of the committed BASELINE sweep (profiles/
+    sweep_baseline_configs.md, made by bench.py --sweep and
+    cost_model --fit --summary)."""
+    import re
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    fit = {}
+    with open(os.path.join(repo, "profiles", "sweep_baseline_configs.md")) as f:
+        for line in f:
+            m = re.match(r"\| (tiled-v\d+-(kn|nk|g)) \| ([0-9.]+) \|", line)
+            if m:
+                fit[m.group(1)] = float(m.group(3))
+    src = open(os.path.join(repo, "cdna3-bench_amd", "csrc", "mxfp4_api.hip")).read()
+    table = {}
+    for m in re.finditer(r"\{\{[0-9, ]+\}, ([0-9.]+), ([0-9.]+), \d, kFamily\w+\},?\s*// (\d+):", src):
+        table[int(m.group(3))] = (float(m.group(1)), float(m.group(2)))
+    for v in (6, 7, 15):
+        assert abs(table[v][0] - fit[f"tiled-v{v}-kn"]) < 0.0015, (v, table[v], fit)
+        assert abs(table[v][1] - fit[f"tiled-v{v}-nk"]) < 0.0015, (v, table[v], fit)
