@@ -182,32 +182,50 @@ __device__ __forceinline__ float load_coherent1(__amdgpu_buffer_rsrc_t r, uint32
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCPolDevice));
 }
 
+// The lane index computed afresh (v_mbcnt) where the optimizer cannot reuse
+// an earlier copy.  A kernel whose main loop takes every VGPR uses it for the
+// lane-derived offsets of its epilogue: kept live across the loop they are
+// spilled, and each reload's vmcnt(0) wait also waits for every store issued
+// before it.
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // Split-K arrival: every thread's SC1 partial stores have completed when
 // thread 0 bumps the tile counter; returns true in the CTA that arrived last
 // (it then owns the reduction and resets the counter for the next call).
-__device__ __forceinline__ bool splitk_arrive_last(uint32_t* counter, uint32_t splits, int* s_flag) {
+// tid: the caller's work-item id.
+__device__ __forceinline__ bool splitk_arrive_last(uint32_t* counter, uint32_t splits, int* s_flag, int tid) {
   wait_vmcnt0();
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = prev == splits - 1;
     if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *s_flag = last;
   }
   __syncthreads();
-  return *s_flag != 0;
+  // the same word for every thread: wave-uniform to the compiler, so code
+  // after a return on it keeps its values in SGPRs
+  return __builtin_amdgcn_readfirstlane(*s_flag) != 0;
+}
+__device__ __forceinline__ bool splitk_arrive_last(uint32_t* counter, uint32_t splits, int* s_flag) {
+  return splitk_arrive_last(counter, splits, s_flag, (int)threadIdx.x);
 }
 
 // The last CTA's sum of a tile's split partials: Q f32x4 per thread, element
-// i of split sp at byte sp * slot + (i * nt + threadIdx.x) * 16.  Each
+// i of split sp at byte sp * slot + (i * nt + tid) * 16 (tid: the work-item
+// id; splitk_sum passes threadIdx.x).  Each
 // element's splits are added in split order (bit-reproducible).  The loads go
 // GRP elements at a time, one split's GRP loads in flight together: S * Q /
 // GRP memory round trips (an element-by-element loop waited for every load,
 // S * Q round trips -- 160 us of tail at S = 16).  put(i, sum) stores the
 // result.
 template <int Q, int GRP = 8, typename Put>
-__device__ __forceinline__ void splitk_sum(__amdgpu_buffer_rsrc_t rp, uint32_t slot, int splits, uint32_t nt,
-                                           Put&& put) {
+__device__ __forceinline__ void splitk_sum_tid(__amdgpu_buffer_rsrc_t rp, uint32_t slot, int splits, uint32_t nt,
+                                               int tid, Put&& put) {
   static_assert(Q % GRP == 0, "whole groups");
 #pragma unroll
   for (int g0 = 0; g0 < Q; g0 += GRP) {
@@ -216,13 +234,18 @@ __device__ __forceinline__ void splitk_sum(__amdgpu_buffer_rsrc_t rp, uint32_t s
       f32x4 t[GRP];
 #pragma unroll
       for (int b = 0; b < GRP; ++b)
-        t[b] = load_coherent4(rp, sp * slot + (uint32_t)((g0 + b) * nt + threadIdx.x) * 16);
+        t[b] = load_coherent4(rp, sp * slot + (uint32_t)((g0 + b) * nt + tid) * 16);
 #pragma unroll
       for (int b = 0; b < GRP; ++b) sum[b] = sp == 0 ? t[b] : sum[b] + t[b];
     }
 #pragma unroll
     for (int b = 0; b < GRP; ++b) put(g0 + b, sum[b]);
   }
+}
+template <int Q, int GRP = 8, typename Put>
+__device__ __forceinline__ void splitk_sum(__amdgpu_buffer_rsrc_t rp, uint32_t slot, int splits, uint32_t nt,
+                                           Put&& put) {
+  splitk_sum_tid<Q, GRP>(rp, slot, splits, nt, (int)threadIdx.x, put);
 }
 
 // ---- split-K partials as tagged packets (streaming and decode kernels) ------

@@ -499,6 +499,15 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
     __syncthreads();
   }
 
+  // Lane-derived values of the epilogue, recomputed here: nothing
+  // lane-derived that only the epilogue reads stays live across the main loop
+  // (which takes all 256 registers; the allocator spilled such values, and
+  // the reloads waited for the C stores issued before them).  wave, wm, wn
+  // are SGPRs.
+  const int lane_e = fresh_lane();
+  const int tid_e = wave * 64 + lane_e;
+  const int ce = lane_e & 15, qe = lane_e >> 4;
+
   // ---- split-K fix-up (the pipelined kernel's protocol) ------------------------
   int* s_last = reinterpret_cast<int*>(smem);
   if (p.splits > 1) {
@@ -510,10 +519,10 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
     for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
       for (int cb = 0; cb < kCB; ++cb)
-        store_coherent(rp, split * SLOT + (uint32_t)((rb * kCB + cb) * kThreads + threadIdx.x) * 16, acc[rb][cb]);
-    if (!splitk_arrive_last(p.counters + tile, (uint32_t)p.splits, s_last)) return;
-    splitk_sum<Q>(rp, SLOT, p.splits, kThreads,
-                  [&](int i, f32x4 v) __attribute__((always_inline)) { acc[i / kCB][i % kCB] = v; });
+        store_coherent(rp, split * SLOT + (uint32_t)((rb * kCB + cb) * kThreads + tid_e) * 16, acc[rb][cb]);
+    if (!splitk_arrive_last(p.counters + tile, (uint32_t)p.splits, s_last, tid_e)) return;
+    splitk_sum_tid<Q>(rp, SLOT, p.splits, kThreads, tid_e,
+                      [&](int i, f32x4 v) __attribute__((always_inline)) { acc[i / kCB][i % kCB] = v; });
   }
 
   // ---- epilogue: 4 adjacent columns (blocks 4g .. 4g+3) per lane and row --------
@@ -529,7 +538,7 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
     if constexpr (kFused) {
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
-        const int col = n0 + wn * 128 + 64 * g + 4 * c;
+        const int col = n0 + wn * 128 + 64 * g + 4 * ce;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           bias[g][j] = -0.0f;
@@ -541,17 +550,24 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
     }
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      const int col = n0 + wn * 128 + 64 * g + 4 * c;
+      const int col = n0 + wn * 128 + 64 * g + 4 * ce;
       if (col >= N) continue;
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int row = m0 + wm * 64 + rb * 16 + 4 * q + i;
+          const int row = m0 + wm * 64 + rb * 16 + 4 * qe + i;
           if (row >= M) continue;
           float v[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) v[j] = acc[rb][4 * g + j][i];
+          if constexpr (decltype(out)::value == 0) {
+            // plain fp32 store: each element copied to a VGPR on its own
+            // (packing the four AGPR elements straight into the store's
+            // register quad went through scratch, four round trips per store)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) asm("" : "+v"(v[j]));
+          }
           if constexpr (kFused) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) v[j] = activate_c<kAct>(v[j] + bias[g][j]);
