@@ -162,6 +162,17 @@ def summarize(trace: str, kernel_re: str, pmc: list[str], copy_bytes: float | No
         if merged.get("SQ_WAIT_INST_ANY") is not None and merged.get("SQ_WAVES"):
             derived.append(f"- cycles a wave waited on any instruction dependency, per wave = "
                            f"{merged['SQ_WAIT_INST_ANY'] / merged['SQ_WAVES']:.0f}")
+        # LDS: SQ_LDS_IDX_ACTIVE and SQ_LDS_BANK_CONFLICT are cycles summed over
+        # CUs, like SQ_BUSY_CU_CYCLES
+        lds_active = merged.get("SQ_LDS_IDX_ACTIVE")
+        if lds_active and merged.get("SQ_BUSY_CU_CYCLES"):
+            result["lds_active_frac"] = lds_active / merged["SQ_BUSY_CU_CYCLES"]
+            derived.append(f"- LDS active per busy CU cycle = SQ_LDS_IDX_ACTIVE / SQ_BUSY_CU_CYCLES = "
+                           f"{100 * lds_active / merged['SQ_BUSY_CU_CYCLES']:.1f}%")
+        if lds_active and merged.get("SQ_LDS_BANK_CONFLICT") is not None:
+            result["lds_conflict_frac"] = merged["SQ_LDS_BANK_CONFLICT"] / lds_active
+            derived.append(f"- LDS bank-conflict cycles / LDS active cycles = "
+                           f"{100 * merged['SQ_LDS_BANK_CONFLICT'] / lds_active:.1f}%")
         if derived:
             lines += ["", "## latency, occupancy, cache", ""] + derived
     if copy_bytes and copy_c and ("FETCH_SIZE" in merged or "WRITE_SIZE" in merged):
