@@ -23,6 +23,9 @@ constexpr double kNumCus = 256.0;
 constexpr double kHbmBytesPerS = 8.0e12;
 constexpr double kMfmaFlopsPerS = 2.5e15;
 constexpr double kLaunchS = 2.0e-6;  // fixed per-launch cost folded into every plan
+// [N,K/2] -> G rewrite of a via-G plan: fraction of HBM bandwidth it moves its
+// bytes (read + write of codes and scales) at
+constexpr double kConvertEff = 0.6;
 
 // Tiled kernel families: the first version (mxfp4_tiled.hip), the pipelined
 // kernel (mxfp4_tiled_pipe.hip) and the hand-scheduled 128 x 256 kernel
@@ -105,6 +108,14 @@ double problem_bytes(int64_t M, int64_t N, int64_t K, int c_bytes) {
   return 2.0 * M * K + N * K / 2.0 + N * K / 32.0 + (double)c_bytes * M * N;
 }
 
+// Workspace bytes of the G copy of a via-G plan (codes, then scales).
+size_t via_g_bytes(int64_t N, int64_t K) {
+  return align_up((size_t)(K / 2) * N, 256) + align_up((size_t)(K / 32) * N, 256);
+}
+bool via_g_ok(int layout, int64_t N, int64_t K) {
+  return layout == kLayoutNK && layout_shape_ok(kLayoutG, N, K) && K % 64 == 0;
+}
+
 int64_t stream_splits(const StreamShape& s, int64_t K) { return ceil_div(K, s.k_split()); }
 int64_t stream_ctas(const StreamShape& s, int64_t N, int64_t K) {
   const int64_t splits = stream_splits(s, K);
@@ -135,7 +146,7 @@ bool gemv_plan_ok(int layout, int64_t M, int64_t N, const GemvShape& g) {
   return gemv_shape_available(layout, g);
 }
 
-void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out);
+void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out, size_t max_ws);
 
 // Memory-bound family.  [N,K/2]: 32 columns x the whole K per CTA of 16
 // waves (no split needed once N >= 8192).  [K/2,N]: 128 columns per CTA and
@@ -178,7 +189,7 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
   if (layout != kLayoutKN && layout != kLayoutNK) {
     // prepacked layouts the streaming kernel does not take: the pipelined
     // tiled kernel with split-K
-    choose_tiled(layout, M, N, K, out);
+    choose_tiled(layout, M, N, K, out, 0);
     return;
   }
   int want;
@@ -258,33 +269,49 @@ double tiled_time(const TiledVariant& v, int layout, int64_t M, int64_t N, int64
   return t + kLaunchS;
 }
 
-void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
+size_t plan_workspace(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_plan& p);
+
+// max_ws: the workspace the call has; a via-G plan ([N,K/2] weights rewritten
+// to G first, at kConvertEff of HBM bandwidth) is a candidate only if its
+// workspace fits.
+void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out, size_t max_ws) {
   double best = 1e30;
-  int bv = 0, bs = 1;
+  int bv = 0, bs = 1, bf = 0;
   const int64_t ksteps = ceil_div(K, 64);
-  for (int v = 0; v < kNumTiled; ++v) {
-    const TiledVariant& tv = kTiled[v];
-    if (!tiled_variant_ok(tv, layout, N, K) || tiled_eff(tv, layout) <= 0.0) continue;
-    const int64_t tiles = ceil_div(M, tv.shape.bm()) * ceil_div(N, tv.shape.bn());
-    for (int s = 1; s <= 16 && s <= ksteps; ++s) {
-      if (s > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) break;
-      const double t = tiled_time(tv, layout, M, N, K, s);
-      if (t < best * 0.98) {  // prefer fewer splits / earlier variants on near ties
-        best = t;
-        bv = v;
-        bs = s;
+  const bool try_g = via_g_ok(layout, N, K);
+  const double t_convert =
+      2.0 * ((double)(K / 2) * N + (double)(K / 32) * N) / (kHbmBytesPerS * kConvertEff) + kLaunchS;
+  for (int pass = 0; pass < (try_g ? 2 : 1); ++pass) {
+    const int lay = pass == 0 ? layout : kLayoutG;
+    for (int v = 0; v < kNumTiled; ++v) {
+      const TiledVariant& tv = kTiled[v];
+      if (!tiled_variant_ok(tv, lay, N, K) || tiled_eff(tv, lay) <= 0.0) continue;
+      const int64_t tiles = ceil_div(M, tv.shape.bm()) * ceil_div(N, tv.shape.bn());
+      for (int s = 1; s <= 16 && s <= ksteps; ++s) {
+        if (s > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) break;
+        if (pass == 1 && plan_workspace(layout, M, N, K, {MXFP4_KERNEL_TILED, v, s, MXFP4_PLAN_TILED_VIA_G}) > max_ws)
+          continue;
+        const double t = tiled_time(tv, lay, M, N, K, s) + (pass == 1 ? t_convert : 0.0);
+        if (t < best * 0.98) {  // prefer fewer splits / earlier variants / no rewrite on near ties
+          best = t;
+          bv = v;
+          bs = s;
+          bf = pass == 1 ? MXFP4_PLAN_TILED_VIA_G : 0;
+        }
       }
     }
   }
   out->kernel = MXFP4_KERNEL_TILED;
   out->variant = bv;
   out->split_k = bs;
-  out->flags = 0;
+  out->flags = bf;
 }
 
 hipError_t validate_plan(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_plan& p) {
   if (p.split_k < 1) return hipErrorInvalidValue;
-  if (p.flags & ~MXFP4_PLAN_STREAM_NO_POLL) return hipErrorInvalidValue;
+  if (p.flags & ~(MXFP4_PLAN_STREAM_NO_POLL | MXFP4_PLAN_TILED_VIA_G)) return hipErrorInvalidValue;
+  if ((p.flags & MXFP4_PLAN_TILED_VIA_G) && (p.kernel != MXFP4_KERNEL_TILED || !via_g_ok(layout, N, K)))
+    return hipErrorInvalidValue;
   switch (p.kernel) {
     case MXFP4_KERNEL_GENERIC:
       return hipSuccess;
@@ -307,7 +334,8 @@ hipError_t validate_plan(int layout, int64_t M, int64_t N, int64_t K, const mxfp
     case MXFP4_KERNEL_TILED: {
       if (p.variant < 0 || p.variant >= kNumTiled) return hipErrorInvalidValue;
       if (layout == kLayoutKN && N % 16 != 0) return hipErrorInvalidValue;
-      if (!tiled_variant_ok(kTiled[p.variant], layout, N, K)) return hipErrorInvalidValue;
+      const int lay = (p.flags & MXFP4_PLAN_TILED_VIA_G) ? kLayoutG : layout;
+      if (!tiled_variant_ok(kTiled[p.variant], lay, N, K)) return hipErrorInvalidValue;
       const TiledShape& s = kTiled[p.variant].shape;
       const int64_t tiles = ceil_div(M, s.bm()) * ceil_div(N, s.bn());
       if (p.split_k > 1 && tiles * 4 > (int64_t)MXFP4_COUNTER_BYTES) return hipErrorInvalidValue;
@@ -319,17 +347,31 @@ hipError_t validate_plan(int layout, int64_t M, int64_t N, int64_t K, const mxfp
   }
 }
 
-void auto_plan(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
+// max_ws: the workspace bytes the call can use beyond what the direct plans
+// need (only via-G plans are held to it)
+void auto_plan(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out, size_t max_ws) {
   if (layout == kLayoutKN && N % 16 != 0) {
     *out = {MXFP4_KERNEL_GENERIC, 0, 1, 0};
   } else if (M <= 32) {
     choose_gemv(layout, M, N, K, out);
   } else {
-    choose_tiled(layout, M, N, K, out);
+    choose_tiled(layout, M, N, K, out, max_ws);
   }
 }
 
+// [split-K counters][partials] (split_k > 1), then a via-G plan's G copy.
+// The G copy starts after the counter region even at split 1: a workspace is
+// shared by the calls on its stream (the extension keeps one per stream), and
+// every split-K call needs the counters zero on entry.
+size_t split_workspace(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_plan& p);
+size_t via_g_offset(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_plan& p) {
+  return std::max<size_t>(split_workspace(layout, M, N, K, p), MXFP4_COUNTER_BYTES);
+}
 size_t plan_workspace(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_plan& p) {
+  if (p.flags & MXFP4_PLAN_TILED_VIA_G) return via_g_offset(layout, M, N, K, p) + via_g_bytes(N, K);
+  return split_workspace(layout, M, N, K, p);
+}
+size_t split_workspace(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_plan& p) {
   if (p.split_k <= 1) return 0;
   size_t partial = 0;
   if (p.kernel == MXFP4_KERNEL_GEMV) {
@@ -392,6 +434,9 @@ hipError_t make_epilogue(const mxfp4_epilogue* in, Epilogue* out) {
 hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c_dtype, int64_t M,
                int64_t N, int64_t K, int layout, const mxfp4_plan* plan_in, const mxfp4_epilogue* ep_in,
                void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  // an automatic plan may rewrite [N,K/2] weights to G only in a workspace
+  // the caller passed
+  const size_t max_ws = workspace && aligned16(workspace) ? workspace_bytes : 0;
   hipError_t e = check_args(A, B, S, C, c_dtype, M, N, K, layout);
   if (e != hipSuccess) return e;
   Epilogue ep;
@@ -409,7 +454,7 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
   if (plan_in && plan_in->kernel != MXFP4_KERNEL_AUTO) {
     plan = *plan_in;
   } else {
-    auto_plan(layout, M, N, K, &plan);
+    auto_plan(layout, M, N, K, &plan, max_ws);
   }
   // The fast families read 16-byte vectors.
   if (plan.kernel != MXFP4_KERNEL_GENERIC &&
@@ -424,8 +469,19 @@ hipError_t run(const void* A, const uint8_t* B, const uint8_t* S, void* C, int c
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
     return hipErrorInvalidValue;
   uint32_t* counters = static_cast<uint32_t*>(workspace);
+  const size_t split_need = split_workspace(layout, M, N, K, plan);
   float* partials =
-      need ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + MXFP4_COUNTER_BYTES) : nullptr;
+      split_need ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + MXFP4_COUNTER_BYTES) : nullptr;
+  if (plan.flags & MXFP4_PLAN_TILED_VIA_G) {
+    // the G copy after the split-K region; the tiled kernel then reads it
+    uint8_t* g_codes = static_cast<uint8_t*>(workspace) + via_g_offset(layout, M, N, K, plan);
+    uint8_t* g_scales = g_codes + align_up((size_t)(K / 2) * N, 256);
+    e = launch_convert_nk_to_g(B, S, g_codes, g_scales, (size_t)K, (size_t)N, stream);
+    if (e != hipSuccess) return e;
+    B = g_codes;
+    S = g_scales;
+    layout = kLayoutG;
+  }
 
   const uint16_t* A16 = static_cast<const uint16_t*>(A);
   switch (plan.kernel) {
@@ -544,7 +600,7 @@ extern "C" {
 hipError_t mxfp4_select_plan(int64_t M, int64_t N, int64_t K, int b_layout, mxfp4_plan* out) {
   if (!out || M < 0 || N < 0 || K < 0 || K % 32 != 0) return hipErrorInvalidValue;
   if (!layout_ok(b_layout, N, K)) return hipErrorInvalidValue;
-  auto_plan(b_layout, M, N, K, out);
+  auto_plan(b_layout, M, N, K, out, SIZE_MAX);
   return hipSuccess;
 }
 
@@ -576,14 +632,15 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
     case MXFP4_KERNEL_TILED: {
       if (plan->variant < 0 || plan->variant >= kNumTiled) return hipErrorInvalidValue;
       const TiledShape& s = kTiled[plan->variant].shape;
+      const char* via = (plan->flags & MXFP4_PLAN_TILED_VIA_G) ? " via-g" : "";
       if (kTiled[plan->variant].family == kFamilySched)
-        snprintf(buf, buf_len, "tiled-sched %dx%d w%dx%d ns%d split%d", s.bm(), s.bn(), s.wm, s.wn,
-                 s.stages, plan->split_k);
+        snprintf(buf, buf_len, "tiled-sched %dx%d w%dx%d ns%d split%d%s", s.bm(), s.bn(), s.wm, s.wn,
+                 s.stages, plan->split_k, via);
       else if (kTiled[plan->variant].family == kFamilyPipe)
-        snprintf(buf, buf_len, "tiled-pipe %dx%d w%dx%d ns%d split%d", s.bm(), s.bn(), s.wm, s.wn,
-                 s.stages, plan->split_k);
+        snprintf(buf, buf_len, "tiled-pipe %dx%d w%dx%d ns%d split%d%s", s.bm(), s.bn(), s.wm, s.wn,
+                 s.stages, plan->split_k, via);
       else
-        snprintf(buf, buf_len, "tiled %dx%d w%dx%d split%d", s.bm(), s.bn(), s.wm, s.wn, plan->split_k);
+        snprintf(buf, buf_len, "tiled %dx%d w%dx%d split%d%s", s.bm(), s.bn(), s.wm, s.wn, plan->split_k, via);
       return hipSuccess;
     }
     default:
@@ -600,7 +657,7 @@ size_t mxfp4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int b_layout,
     p = *plan;
     if (validate_plan(b_layout, M, N, K, p) != hipSuccess) return 0;
   } else {
-    auto_plan(b_layout, M, N, K, &p);
+    auto_plan(b_layout, M, N, K, &p, SIZE_MAX);
   }
   return plan_workspace(b_layout, M, N, K, p);
 }
@@ -695,7 +752,14 @@ hipError_t mxfp4_gemm_noalloc(const void* A, const uint8_t* B, const uint8_t* S,
   void* ws = nullptr;
   e = noalloc_scratch(stream, &ws);
   if (e != hipSuccess) return e;
-  const size_t need = mxfp4_gemm_workspace_bytes(M, N, K, b_layout, nullptr);
+  // the automatic plan as run() picks it with this workspace: a via-G
+  // rewrite only if its G copy fits the scratch
+  size_t need = 0;
+  if (M > 0 && N > 0 && K > 0) {
+    mxfp4_plan p;
+    auto_plan(b_layout, M, N, K, &p, MXFP4_NOALLOC_SCRATCH_BYTES);
+    need = plan_workspace(b_layout, M, N, K, p);
+  }
   if (need > MXFP4_NOALLOC_SCRATCH_BYTES) return hipErrorOutOfMemory;
   return run(A, B, S, C, c_dtype, M, N, K, b_layout, nullptr, nullptr, ws, MXFP4_NOALLOC_SCRATCH_BYTES, stream);
 }

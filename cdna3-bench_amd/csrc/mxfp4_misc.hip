@@ -146,6 +146,51 @@ __global__ void __launch_bounds__(256) convert_scales_kernel(const uint8_t* __re
   }
 }
 
+// [N,K/2] -> G without byte gathers (the rewrite a via-G GEMM plan runs
+// before the tiled kernel, and convert_layout's path for this pair): one
+// workgroup per 128-column block and 64 code dwords (512 K) with their 16
+// scale groups, transposed through LDS so that the reads (256 contiguous
+// bytes of a column) and the writes (a G chunk row: 512 contiguous bytes)
+// are whole lines.  B 16-byte aligned, B_out 4-byte aligned, N % 128 == 0.
+constexpr int kCvW = 64;  // code dwords (8 K each) per workgroup
+__global__ void __launch_bounds__(256) convert_nk_to_g_kernel(const uint8_t* __restrict__ B,
+                                                               const uint8_t* __restrict__ S,
+                                                               uint8_t* __restrict__ B_out,
+                                                               uint8_t* __restrict__ S_out, int K) {
+  // [column][dword] padded to 65 words: the transposed reads (128 columns of
+  // one dword) fall on 32 distinct banks; scales [column][group] in 20-byte
+  // rows (5 words: odd, so 32 consecutive columns hit 32 banks)
+  __shared__ uint32_t t[kGCols][kCvW + 1];
+  __shared__ uint8_t ts[kGCols][kCvW / 4 + 4];
+  const size_t nb = blockIdx.x;
+  const int kw = K / 8, gk = K / 32;
+  const int w0 = (int)blockIdx.y * kCvW;
+  const int nw = min(kCvW, kw - w0);  // a multiple of 4 (K % 32 == 0)
+  const int g0 = w0 / 4, ng = nw / 4;
+  for (int i = threadIdx.x; i < kGCols * 16; i += 256) {
+    const int col = i >> 4, j = (i & 15) * 4;
+    if (j < nw) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(B + (nb * kGCols + col) * (size_t)(K / 2) + (size_t)(w0 + j) * 4);
+      t[col][j] = v.x;
+      t[col][j + 1] = v.y;
+      t[col][j + 2] = v.z;
+      t[col][j + 3] = v.w;
+    }
+    const int g = i & 15;
+    if (g < ng) ts[col][g] = S[(nb * kGCols + col) * (size_t)gk + g0 + g];
+  }
+  __syncthreads();
+  uint32_t* out = reinterpret_cast<uint32_t*>(B_out);
+  for (int i = threadIdx.x; i < kCvW * kGCols; i += 256) {
+    const int w = i >> 7, col = i & 127;
+    if (w < nw) out[(nb * kw + w0 + w) * kGCols + col] = t[col][w];
+  }
+  for (int i = threadIdx.x; i < (kCvW / 4) * kGCols; i += 256) {
+    const int g = i >> 7, col = i & 127;
+    if (g < ng) S_out[(nb * gk + g0 + g) * kGCols + col] = ts[col][g];
+  }
+}
+
 // 16 bytes per thread; vector stores when p is 16-byte aligned (C may be a
 // view at any element offset), byte stores otherwise and for the tail.
 __global__ void __launch_bounds__(256) zero_fill_kernel(uint8_t* p, size_t bytes) {
@@ -203,6 +248,10 @@ struct ConvertFrom {
   struct To {
     static hipError_t run(const uint8_t* B, const uint8_t* S, uint8_t* B_out, uint8_t* S_out,
                           size_t K, size_t N, hipStream_t stream) {
+      if constexpr (SRC == kLayoutNK && DST == kLayoutG) {
+        if (((uintptr_t)B & 15u) == 0 && ((uintptr_t)B_out & 3u) == 0 && K <= (size_t)INT32_MAX)
+          return launch_convert_nk_to_g(B, S, B_out, S_out, K, N, stream);
+      }
       const size_t vecs = K / 2 * N / 16, sbytes = K / 32 * N;
       hipLaunchKernelGGL((convert_codes_kernel<SRC, DST>), dim3(grid_for(vecs)),
                          dim3(256), 0, stream, B, B_out, K, N);
@@ -242,6 +291,17 @@ hipError_t launch_convert(int src_layout, int dst_layout, const uint8_t* B, cons
                           uint8_t* B_out, uint8_t* S_out, size_t K, size_t N, hipStream_t stream) {
   if (K * N == 0) return hipSuccess;
   return by_layout<ConvertLaunch>(src_layout, dst_layout, B, S, B_out, S_out, K, N, stream);
+}
+
+hipError_t launch_convert_nk_to_g(const uint8_t* B, const uint8_t* S, uint8_t* B_out, uint8_t* S_out, size_t K,
+                                  size_t N, hipStream_t stream) {
+  if (K * N == 0) return hipSuccess;
+  if (N % kGCols != 0 || K % 32 != 0 || K > (size_t)INT32_MAX || N / kGCols > (size_t)INT32_MAX ||
+      ((uintptr_t)B & 15u) != 0 || ((uintptr_t)B_out & 3u) != 0)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(N / kGCols), (unsigned)((K / 8 + kCvW - 1) / kCvW));
+  hipLaunchKernelGGL(convert_nk_to_g_kernel, grid, dim3(256), 0, stream, B, S, B_out, S_out, (int)K);
+  return hipGetLastError();
 }
 
 hipError_t launch_zero_fill(void* C, size_t bytes, hipStream_t stream) {

@@ -77,6 +77,22 @@ typedef struct mxfp4_plan {
 #define MXFP4_PLAN_STREAM_NO_POLL 1
 
 /*
+ * Plan flag for MXFP4_KERNEL_TILED with [N,K/2] weights, N % 128 == 0 and
+ * K % 64 == 0: the call first rewrites the weights to the G layout in the
+ * workspace (after the split-K counters and partials -- the counter region
+ * is kept even at split 1, as the workspace may serve other calls: K/2 * N
+ * code bytes and K/32 * N scale bytes, each rounded up to 256), then runs the
+ * tiled variant on G.  The
+ * [N,K/2] operand reads of the tiled kernels are 2-way LDS bank-conflicted;
+ * for MFMA-bound shapes the rewrite costs less than it saves.  The automatic
+ * plan sets it when the cost model says so and the workspace holds it
+ * (mxfp4_gemm_workspace_bytes with a NULL plan counts it; a call with a
+ * smaller or no workspace gets the direct plan).  Results are bit-identical
+ * to the direct plan's.
+ */
+#define MXFP4_PLAN_TILED_VIA_G 2
+
+/*
  * Fused epilogue: C = act(A x W + bias) + residual, in fp32, then rounded to
  * C's dtype.  act: SiLU x / (1 + e^-x); GELU 0.5 x (1 + erf(x / sqrt 2));
  * GELU-tanh 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) -- the

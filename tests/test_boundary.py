@@ -266,4 +266,35 @@ def test_stream_packets_must_fit_one_descriptor(lib):
 def test_plan_flags_validated(lib):
     ws = lib.mxfp4_gemm_workspace_bytes
     assert ws(16, 8192, 8192, 1, ctypes.byref(Plan(4, 3, 2, 1))) > 0   # MXFP4_PLAN_STREAM_NO_POLL
-    assert ws(16, 8192, 8192, 1, ctypes.byref(Plan(4, 3, 2, 2))) == 0  # unknown flag bit
+    assert ws(16, 8192, 8192, 1, ctypes.byref(Plan(4, 3, 2, 2))) == 0  # MXFP4_PLAN_TILED_VIA_G on a stream plan
+    assert ws(16, 8192, 8192, 1, ctypes.byref(Plan(4, 3, 2, 4))) == 0  # unknown flag bit
+
+
+def _via_g_bytes(N, K):
+    up = lambda v: (v + 255) // 256 * 256
+    return up(K // 2 * N) + up(K // 32 * N)
+
+
+def test_via_g_plans(lib, kk):
+    """MXFP4_PLAN_TILED_VIA_G: the workspace is the split-K region followed by
+    the G copy of the weights; the flag is valid only for tiled plans on
+    [N,K/2] weights that G can hold (N % 128 == 0, K % 64 == 0); the
+    automatic plan uses it for the MFMA-bound BASELINE shapes, where the
+    rewrite costs less than the [N,K/2] operand reads' bank conflicts."""
+    ws = lib.mxfp4_gemm_workspace_bytes
+    M, N, K = 4096, 12288, 3072
+    # the G copy starts after the split-K counters even at split 1 (a workspace
+    # shared with split-K calls keeps its counters zero)
+    assert ws(M, N, K, 1, ctypes.byref(Plan(2, 15, 1, 2))) == (1 << 20) + _via_g_bytes(N, K)
+    two = ws(M, N, K, 1, ctypes.byref(Plan(2, 15, 2, 0)))
+    assert two > 0 and ws(M, N, K, 1, ctypes.byref(Plan(2, 15, 2, 2))) == two + _via_g_bytes(N, K)
+    assert ws(M, N, K, 0, ctypes.byref(Plan(2, 15, 1, 2))) == 0       # [K/2,N]
+    assert ws(M, 12160 + 64, K, 1, ctypes.byref(Plan(2, 15, 1, 2))) == 0  # N % 128 != 0
+    assert ws(M, N, 3072 + 32, 1, ctypes.byref(Plan(2, 15, 1, 2))) == 0   # K % 64 != 0
+    for shape in [(4096, 12288, 3072), (4608, 3072, 12288), (2048, 28672, 8192), (8192, 28672, 8192)]:
+        desc = kk.select_plan(*shape, "nk")[3]
+        assert desc.endswith("via-g"), (shape, desc)
+        assert ws(*shape, 1, None) >= _via_g_bytes(shape[1], shape[2])
+    for shape in [(128, 28672, 8192), (512, 28672, 8192)]:
+        assert not kk.select_plan(*shape, "nk")[3].endswith("via-g"), shape
+    assert not kk.select_plan(4096, 12288, 3072, "kn")[3].endswith("via-g")

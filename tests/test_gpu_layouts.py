@@ -48,7 +48,9 @@ def _host(B, S, layout):
     return np.ascontiguousarray(X), np.ascontiguousarray(Xs)
 
 
-@pytest.mark.parametrize("K,N", [(64, 128), (192, 384), (1024, 256)])
+# [N,K/2] -> G conversion tiles hold 64 code dwords (512 K): K = 64 and 192
+# fill one partly, 1024 two exactly, 4160 eight and a partial ninth
+@pytest.mark.parametrize("K,N", [(64, 128), (192, 384), (1024, 256), (4160, 256)])
 def test_convert_layout_every_pair(kk, K, N):
     import torch
 
@@ -128,6 +130,46 @@ def test_tiled_prepacked_equals_base_layout(kk, pre, base, K):
             b = run_gemm(kk, A_bits, W, S, base, torch.float32, plan=plan)
             assert np.array_equal(a, b), f"variant {v} split {split}"
             assert mo.strict_violations(a, ref, K) == 0
+
+
+VIA_G = 2  # MXFP4_PLAN_TILED_VIA_G
+
+
+@pytest.mark.parametrize("M,N,K,split", [(300, 512, 640, 1), (300, 512, 640, 2), (130, 1280, 4224, 3)])
+def test_tiled_via_g_equals_direct_nk(kk, M, N, K, split):
+    """A via-G plan ([N,K/2] weights rewritten to G in the workspace, after
+    the split-K region, then the scheduled kernel on G) is bit-identical to
+    the same scheduled plan on the [N,K/2] weights -- both feed the MFMAs
+    the same operands in the same K order -- and meets the tolerance.  The
+    cases run in order on one stream's workspace: a split-K call after a
+    split-1 via-G call finds its counters zero (the G copy once overwrote
+    them)."""
+    import torch
+
+    A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=M + K)
+    ref = oracle_f64(A_bits, W, S)
+    log(f"case via-g M={M} N={N} K={K} split={split}")
+    plan = (kk.KERNEL_TILED, 15, split)
+    a = run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan + (VIA_G,))
+    b = run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan)
+    assert np.array_equal(a, b)
+    assert mo.strict_violations(a, ref, K) == 0
+    c = run_gemm(kk, A_bits, W, S, "nk", torch.bfloat16, plan=plan + (VIA_G,))
+    d = run_gemm(kk, A_bits, W, S, "nk", torch.bfloat16, plan=plan)
+    assert np.array_equal(c, d)
+
+
+def test_tiled_via_g_rejected_where_g_cannot_hold_the_weights(kk):
+    import torch
+
+    A_bits, W, S = mo.make_inputs(64, 320, 640, 118, 134, seed=5)  # N % 128 != 0
+    log("case via-g rejected N=320")
+    with pytest.raises(RuntimeError):
+        run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=(kk.KERNEL_TILED, 15, 1, VIA_G))
+    A_bits, W, S = mo.make_inputs(64, 256, 640, 118, 134, seed=6)
+    with pytest.raises(RuntimeError):  # [K/2,N] weights: the flag is for [N,K/2] only
+        run_gemm(kk, A_bits, W, S, "kn", torch.float32, plan=(kk.KERNEL_TILED, 15, 1, VIA_G))
+    torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("M", [16, 300])
