@@ -59,8 +59,8 @@ const TiledVariant kTiled[] = {
     {{1, 2, 2}, 0.17, 0.15, 2, kFamilyPlain},       // 3:  64 x 256 (re-measured at M = 64 .. 256)
     {{2, 1, 2}, 0.0, 0.0, 2, kFamilyPlain},         // 4: 128 x 128
     {{1, 2, 1}, 0.15, 0.13, 4, kFamilyPlain},       // 5:  32 x 256 (re-measured at M = 48 .. 1024)
-    {{4, 2, 2, 4, 3}, 0.513, 0.472, 1, kFamilyPipe}, // 6: pipelined 256 x 256, 8 waves of 64 x 128, 3 stages
-    {{2, 2, 2, 4, 3}, 0.420, 0.390, 1, kFamilyPipe}, // 7: pipelined 128 x 256, 4 waves of 64 x 128
+    {{4, 2, 2, 4, 3}, 0.505, 0.467, 1, kFamilyPipe}, // 6: pipelined 256 x 256, 8 waves of 64 x 128, 3 stages
+    {{2, 2, 2, 4, 3}, 0.426, 0.382, 1, kFamilyPipe}, // 7: pipelined 128 x 256, 4 waves of 64 x 128
     {{4, 2, 2, 4, 3}, 0.0, 0.0, 1, kFamilyPipe},   // 8: = 6 (a 4-stage 256 x 256 ring no longer fits 160 KB)
     {{2, 4, 4, 2, 3}, 0.0, 0.0, 1, kFamilyPipe},   // 9: = 10
     {{2, 4, 4, 2, 3}, 0.0, 0.0, 1, kFamilyPipe},   // 10: pipelined 256 x 256, 8 waves of 128 x 64, 3 stages
@@ -68,7 +68,7 @@ const TiledVariant kTiled[] = {
     {{2, 4, 2, 2, 4}, 0.0, 0.0, 1, kFamilyPipe},   // 12: pipelined 128 x 256, 8 waves of 64 x 64
     {{1, 4, 4, 2, 4}, 0.0, 0.0, 1, kFamilyPipe},   // 13: pipelined 128 x 256, 4 waves of 128 x 64
     {{2, 1, 2, 4, 4}, 0.0, 0.0, 2, kFamilyPipe},   // 14: pipelined 128 x 128, 2 waves
-    {{2, 2, 2, 4, 3}, 0.546, 0.489, 2, kFamilySched}, // 15: hand-scheduled 128 x 256, 4 waves of 64 x 128, 2 CTAs / CU
+    {{2, 2, 2, 4, 3}, 0.553, 0.482, 2, kFamilySched}, // 15: hand-scheduled 128 x 256, 4 waves of 64 x 128, 2 CTAs / CU
 };
 constexpr int kNumTiled = sizeof(kTiled) / sizeof(kTiled[0]);
 

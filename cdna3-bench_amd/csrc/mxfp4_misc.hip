@@ -148,46 +148,51 @@ __global__ void __launch_bounds__(256) convert_scales_kernel(const uint8_t* __re
 
 // [N,K/2] -> G without byte gathers (the rewrite a via-G GEMM plan runs
 // before the tiled kernel, and convert_layout's path for this pair): one
-// workgroup per 128-column block and 64 code dwords (512 K) with their 16
-// scale groups, transposed through LDS so that the reads (256 contiguous
-// bytes of a column) and the writes (a G chunk row: 512 contiguous bytes)
-// are whole lines.  B 16-byte aligned, B_out 4-byte aligned, N % 128 == 0.
+// workgroup per 32 columns (a quarter of a G block) and 64 code dwords (512
+// K) with their 16 scale groups, transposed through LDS so that the reads
+// (256 contiguous bytes of a column) and the writes (the 32 columns of a G
+// chunk row: 128 contiguous bytes) are whole lines; small tiles keep ~9
+// workgroups per CU in flight on dit_up-sized weights.  B 16-byte aligned,
+// B_out 4-byte aligned, N % 128 == 0.
 constexpr int kCvW = 64;  // code dwords (8 K each) per workgroup
+constexpr int kCvC = 32;  // columns per workgroup
 __global__ void __launch_bounds__(256) convert_nk_to_g_kernel(const uint8_t* __restrict__ B,
                                                                const uint8_t* __restrict__ S,
                                                                uint8_t* __restrict__ B_out,
                                                                uint8_t* __restrict__ S_out, int K) {
-  // [column][dword] padded to 65 words: the transposed reads (128 columns of
+  // [column][dword] padded to 65 words: the transposed reads (32 columns of
   // one dword) fall on 32 distinct banks; scales [column][group] in 20-byte
   // rows (5 words: odd, so 32 consecutive columns hit 32 banks)
-  __shared__ uint32_t t[kGCols][kCvW + 1];
-  __shared__ uint8_t ts[kGCols][kCvW / 4 + 4];
-  const size_t nb = blockIdx.x;
+  __shared__ uint32_t t[kCvC][kCvW + 1];
+  __shared__ uint8_t ts[kCvC][kCvW / 4 + 4];
+  const size_t n0 = (size_t)blockIdx.x * kCvC;  // first column
+  const size_t nb = n0 / kGCols;
+  const int c0 = (int)(n0 % kGCols);              // its place in the G block
   const int kw = K / 8, gk = K / 32;
   const int w0 = (int)blockIdx.y * kCvW;
   const int nw = min(kCvW, kw - w0);  // a multiple of 4 (K % 32 == 0)
   const int g0 = w0 / 4, ng = nw / 4;
-  for (int i = threadIdx.x; i < kGCols * 16; i += 256) {
+  for (int i = threadIdx.x; i < kCvC * 16; i += 256) {
     const int col = i >> 4, j = (i & 15) * 4;
     if (j < nw) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(B + (nb * kGCols + col) * (size_t)(K / 2) + (size_t)(w0 + j) * 4);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(B + (n0 + col) * (size_t)(K / 2) + (size_t)(w0 + j) * 4);
       t[col][j] = v.x;
       t[col][j + 1] = v.y;
       t[col][j + 2] = v.z;
       t[col][j + 3] = v.w;
     }
     const int g = i & 15;
-    if (g < ng) ts[col][g] = S[(nb * kGCols + col) * (size_t)gk + g0 + g];
+    if (g < ng) ts[col][g] = S[(n0 + col) * (size_t)gk + g0 + g];
   }
   __syncthreads();
   uint32_t* out = reinterpret_cast<uint32_t*>(B_out);
-  for (int i = threadIdx.x; i < kCvW * kGCols; i += 256) {
-    const int w = i >> 7, col = i & 127;
-    if (w < nw) out[(nb * kw + w0 + w) * kGCols + col] = t[col][w];
+  for (int i = threadIdx.x; i < kCvW * kCvC; i += 256) {
+    const int w = i >> 5, col = i & 31;
+    if (w < nw) out[(nb * kw + w0 + w) * kGCols + c0 + col] = t[col][w];
   }
-  for (int i = threadIdx.x; i < (kCvW / 4) * kGCols; i += 256) {
-    const int g = i >> 7, col = i & 127;
-    if (g < ng) S_out[(nb * gk + g0 + g) * kGCols + col] = ts[col][g];
+  for (int i = threadIdx.x; i < (kCvW / 4) * kCvC; i += 256) {
+    const int g = i >> 5, col = i & 31;
+    if (g < ng) S_out[(nb * gk + g0 + g) * kGCols + c0 + col] = ts[col][g];
   }
 }
 
@@ -296,10 +301,10 @@ hipError_t launch_convert(int src_layout, int dst_layout, const uint8_t* B, cons
 hipError_t launch_convert_nk_to_g(const uint8_t* B, const uint8_t* S, uint8_t* B_out, uint8_t* S_out, size_t K,
                                   size_t N, hipStream_t stream) {
   if (K * N == 0) return hipSuccess;
-  if (N % kGCols != 0 || K % 32 != 0 || K > (size_t)INT32_MAX || N / kGCols > (size_t)INT32_MAX ||
+  if (N % kGCols != 0 || K % 32 != 0 || K > (size_t)INT32_MAX || N / kCvC > (size_t)INT32_MAX ||
       ((uintptr_t)B & 15u) != 0 || ((uintptr_t)B_out & 3u) != 0)
     return hipErrorInvalidValue;
-  const dim3 grid((unsigned)(N / kGCols), (unsigned)((K / 8 + kCvW - 1) / kCvW));
+  const dim3 grid((unsigned)(N / kCvC), (unsigned)((K / 8 + kCvW - 1) / kCvW));
   hipLaunchKernelGGL(convert_nk_to_g_kernel, grid, dim3(256), 0, stream, B, S, B_out, S_out, (int)K);
   return hipGetLastError();
 }
