@@ -160,8 +160,8 @@ hipError_t launch_convert(int src_layout, int dst_layout, const uint8_t* B, cons
 hipError_t launch_quantize(const void* X, int x_bf16, int x_layout, uint8_t* B, uint8_t* S, int b_layout,
                            size_t K, size_t N, hipStream_t stream);
 
-// [N,K/2] -> G (codes and scales), N % 128 == 0, B 16-byte aligned, B_out
-// 4-byte aligned.
+// [N,K/2] -> G (codes and scales), N % 128 == 0, B and B_out 16-byte
+// aligned, S_out 4-byte aligned.
 hipError_t launch_convert_nk_to_g(const uint8_t* B, const uint8_t* S, uint8_t* B_out, uint8_t* S_out, size_t K,
                                   size_t N, hipStream_t stream);
 

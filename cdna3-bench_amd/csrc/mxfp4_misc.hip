@@ -151,20 +151,21 @@ __global__ void __launch_bounds__(256) convert_scales_kernel(const uint8_t* __re
 // workgroup per 32 columns (a quarter of a G block) and 64 code dwords (512
 // K) with their 16 scale groups, transposed through LDS so that the reads
 // (256 contiguous bytes of a column) and the writes (the 32 columns of a G
-// chunk row: 128 contiguous bytes) are whole lines; small tiles keep ~9
-// workgroups per CU in flight on dit_up-sized weights.  B 16-byte aligned,
-// B_out 4-byte aligned, N % 128 == 0.
+// chunk row: 128 contiguous bytes) are whole lines, all 16 bytes per lane
+// (scale reads too when a column's 16 groups are 16-byte aligned); small
+// tiles keep ~9 workgroups per CU in flight on dit_up-sized weights.
+// B and B_out 16-byte aligned, N % 128 == 0.
 constexpr int kCvW = 64;  // code dwords (8 K each) per workgroup
 constexpr int kCvC = 32;  // columns per workgroup
 __global__ void __launch_bounds__(256) convert_nk_to_g_kernel(const uint8_t* __restrict__ B,
                                                                const uint8_t* __restrict__ S,
                                                                uint8_t* __restrict__ B_out,
                                                                uint8_t* __restrict__ S_out, int K) {
-  // [column][dword] padded to 65 words: the transposed reads (32 columns of
-  // one dword) fall on 32 distinct banks; scales [column][group] in 20-byte
-  // rows (5 words: odd, so 32 consecutive columns hit 32 banks)
+  // [column][dword] padded to 65 words: a 32-lane pass of the transposed
+  // reads (8 column quads x 4 chunk rows) falls on 32 distinct banks;
+  // scales [column][group] in 20-byte rows
   __shared__ uint32_t t[kCvC][kCvW + 1];
-  __shared__ uint8_t ts[kCvC][kCvW / 4 + 4];
+  __shared__ __attribute__((aligned(16))) uint8_t ts[kCvC][kCvW / 4 + 4];
   const size_t n0 = (size_t)blockIdx.x * kCvC;  // first column
   const size_t nb = n0 / kGCols;
   const int c0 = (int)(n0 % kGCols);              // its place in the G block
@@ -172,6 +173,7 @@ __global__ void __launch_bounds__(256) convert_nk_to_g_kernel(const uint8_t* __r
   const int w0 = (int)blockIdx.y * kCvW;
   const int nw = min(kCvW, kw - w0);  // a multiple of 4 (K % 32 == 0)
   const int g0 = w0 / 4, ng = nw / 4;
+  const bool svec = ng == kCvW / 4 && gk % 16 == 0 && ((uintptr_t)S & 15u) == 0;
   for (int i = threadIdx.x; i < kCvC * 16; i += 256) {
     const int col = i >> 4, j = (i & 15) * 4;
     if (j < nw) {
@@ -181,18 +183,39 @@ __global__ void __launch_bounds__(256) convert_nk_to_g_kernel(const uint8_t* __r
       t[col][j + 2] = v.z;
       t[col][j + 3] = v.w;
     }
-    const int g = i & 15;
-    if (g < ng) ts[col][g] = S[(n0 + col) * (size_t)gk + g0 + g];
+  }
+  if (svec) {
+    if (threadIdx.x < kCvC) {
+      const int col = threadIdx.x;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(S + (n0 + col) * (size_t)gk + g0);
+      uint32_t* r = reinterpret_cast<uint32_t*>(&ts[col][0]);  // 20-byte rows: 4-byte aligned
+      r[0] = v.x;
+      r[1] = v.y;
+      r[2] = v.z;
+      r[3] = v.w;
+    }
+  } else {
+    for (int i = threadIdx.x; i < kCvC * 16; i += 256) {
+      const int col = i >> 4, g = i & 15;
+      if (g < ng) ts[col][g] = S[(n0 + col) * (size_t)gk + g0 + g];
+    }
   }
   __syncthreads();
-  uint32_t* out = reinterpret_cast<uint32_t*>(B_out);
-  for (int i = threadIdx.x; i < kCvW * kCvC; i += 256) {
-    const int w = i >> 5, col = i & 31;
-    if (w < nw) out[(nb * kw + w0 + w) * kGCols + c0 + col] = t[col][w];
+  // chunk row w, columns 4q .. 4q+3 of the workgroup's 32: one 16-byte store
+  for (int i = threadIdx.x; i < kCvW * (kCvC / 4); i += 256) {
+    const int w = i >> 3, q = i & 7;
+    if (w < nw) {
+      const u32x4 v = {t[4 * q][w], t[4 * q + 1][w], t[4 * q + 2][w], t[4 * q + 3][w]};
+      *reinterpret_cast<u32x4*>(B_out + ((nb * kw + w0 + w) * kGCols + c0 + 4 * q) * 4) = v;
+    }
   }
-  for (int i = threadIdx.x; i < (kCvW / 4) * kCvC; i += 256) {
-    const int g = i >> 5, col = i & 31;
-    if (g < ng) S_out[(nb * gk + g0 + g) * kGCols + c0 + col] = ts[col][g];
+  if (threadIdx.x < (kCvW / 4) * (kCvC / 4)) {
+    const int g = threadIdx.x >> 3, q = threadIdx.x & 7;
+    if (g < ng) {
+      const uint32_t v = (uint32_t)ts[4 * q][g] | (uint32_t)ts[4 * q + 1][g] << 8 |
+                         (uint32_t)ts[4 * q + 2][g] << 16 | (uint32_t)ts[4 * q + 3][g] << 24;
+      *reinterpret_cast<uint32_t*>(S_out + (nb * gk + g0 + g) * kGCols + c0 + 4 * q) = v;
+    }
   }
 }
 
@@ -254,7 +277,8 @@ struct ConvertFrom {
     static hipError_t run(const uint8_t* B, const uint8_t* S, uint8_t* B_out, uint8_t* S_out,
                           size_t K, size_t N, hipStream_t stream) {
       if constexpr (SRC == kLayoutNK && DST == kLayoutG) {
-        if (((uintptr_t)B & 15u) == 0 && ((uintptr_t)B_out & 3u) == 0 && K <= (size_t)INT32_MAX)
+        if (((uintptr_t)B & 15u) == 0 && ((uintptr_t)B_out & 15u) == 0 && ((uintptr_t)S_out & 3u) == 0 &&
+            K <= (size_t)INT32_MAX)
           return launch_convert_nk_to_g(B, S, B_out, S_out, K, N, stream);
       }
       const size_t vecs = K / 2 * N / 16, sbytes = K / 32 * N;
@@ -302,7 +326,7 @@ hipError_t launch_convert_nk_to_g(const uint8_t* B, const uint8_t* S, uint8_t* B
                                   size_t N, hipStream_t stream) {
   if (K * N == 0) return hipSuccess;
   if (N % kGCols != 0 || K % 32 != 0 || K > (size_t)INT32_MAX || N / kCvC > (size_t)INT32_MAX ||
-      ((uintptr_t)B & 15u) != 0 || ((uintptr_t)B_out & 3u) != 0)
+      ((uintptr_t)B & 15u) != 0 || ((uintptr_t)B_out & 15u) != 0 || ((uintptr_t)S_out & 3u) != 0)
     return hipErrorInvalidValue;
   const dim3 grid((unsigned)(N / kCvC), (unsigned)((K / 8 + kCvW - 1) / kCvW));
   hipLaunchKernelGGL(convert_nk_to_g_kernel, grid, dim3(256), 0, stream, B, S, B_out, S_out, (int)K);
