@@ -613,6 +613,31 @@ __global__ void __launch_bounds__(kThreads, 2) tiled_sched_kernel(TiledArgs p) {
       }
     }
   };
+  // Interior tiles with a plain bf16 C: one buffer store per lane, row and 4
+  // columns, row offsets in the scalar offset, no bounds checks and no 64-bit
+  // address arithmetic -- about half the epilogue's instructions, which run
+  // once per tile from a cold instruction cache.
+  if constexpr (kOut == 1) {
+    if (m0 + kBM <= M && n0 + kBN <= N && N <= (1 << 22)) {
+      constexpr int kNt = 2;  // non-temporal: C is not read again here
+      const __amdgpu_buffer_rsrc_t rc =
+          make_rsrc(static_cast<uint16_t*>(p.C) + ((size_t)(m0 + wm * 64) * N + n0 + wn * 128));
+      const uint32_t voff = (uint32_t)(4 * qe * N + 4 * ce) * 2;
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t row = (uint32_t)((rb * 16 + i) * N) * 2;
+#pragma unroll
+          for (int g = 0; g < 2; ++g) {
+            const u32x2 w = {pack_bf16x2(acc[rb][4 * g][i], acc[rb][4 * g + 1][i]),
+                             pack_bf16x2(acc[rb][4 * g + 2][i], acc[rb][4 * g + 3][i])};
+            __builtin_amdgcn_raw_buffer_store_b64(w, rc, voff, row + 128u * g, kNt);
+          }
+        }
+      return;
+    }
+  }
   store(StoreKind<kOut == 2>{}, OutKind<kOut>{});
 }
 
