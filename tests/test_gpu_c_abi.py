@@ -220,3 +220,43 @@ def test_graph_capture_workspace(lib):
         eager = kk.gemm(A, B, Sd, None, "nk", torch.float32)  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(eager, want)
+
+
+def test_graph_capture_via_g(lib):
+    """A via-G plan ([N,K/2] weights rewritten to G in the stream's workspace,
+    then the tiled kernel) captured in a HIP graph replays the eager result,
+    replay after replay, with eager work in between."""
+    import torch
+
+    from mxfp4_cdna3 import kernels as kk
+
+    M, N, K = 2048, 4096, 4096
+    log(f"case graph capture via-g M={M} N={N} K={K}")
+    assert kk.select_plan(M, N, K, "nk")[3].endswith("via-g")
+    A_bits, W, S = mo.make_inputs(M, N, K, 122, 130, 1.0, seed=13)
+    A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(W), to_dev_u8(S)
+    want = kk.gemm(A, B, Sd, None, "nk", torch.bfloat16)
+    torch.cuda.synchronize()
+    C = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        kk.gemm(A, B, Sd, C, "nk")  # allocates this stream's workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        kk.gemm(A, B, Sd, C, "nk")
+    for _ in range(3):
+        C.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(C, want)
+        eager = kk.gemm(A, B, Sd, None, "nk", torch.bfloat16)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(eager, want)
+    rows = np.arange(8)
+    cols = np.random.default_rng(13).choice(N, 128, replace=False)
+    ref = oracle_f64(A_bits, W, S, rows, cols)
+    got = want.float().cpu().numpy()[np.ix_(rows, cols)]
+    assert mo.strict_violations(got, ref, K) == 0
