@@ -95,6 +95,8 @@ const StreamShape kStream[] = {
     {1, 16, 2, 1, 1, 256}, // 6: whole K, M <= 16, K <= 4096 (K / 256 waves)
     {1, 8, 4, 0, 8, 512, 16},  // 7: decode kernel, M <= 16, [N,K/2], 64 columns x 4096 K per CTA, K % 512 == 0
     {1, 8, 2, 0, 8, 1024, 8},  // 8: decode kernel, M <= 8, [N,K/2], 32 columns x 8192 K per CTA, K % 1024 == 0
+    {1, 16, 2, 0, 1, 512, 0, 1},  // 9: resident kernel, M == 1, [N,K/2], 32 columns x K <= 8192 per CTA, K % 512 == 0
+    {1, 16, 2, 0, 1, 512, 0, 8},  // 10: resident kernel, M <= 8 (explicit plans only)
 };
 constexpr int kNumStream = sizeof(kStream) / sizeof(kStream[0]);
 constexpr int kStreamSpin = 4096;  // late-unit polls before counter arbitration
@@ -119,10 +121,11 @@ bool via_g_ok(int layout, int64_t N, int64_t K) {
 int64_t stream_splits(const StreamShape& s, int64_t K) { return ceil_div(K, s.k_split()); }
 int64_t stream_ctas(const StreamShape& s, int64_t N, int64_t K) {
   const int64_t splits = stream_splits(s, K);
-  if (s.direct) return ceil_div(N, 16 * s.gcb) * splits;
+  if (s.direct || s.resident) return ceil_div(N, 16 * s.gcb) * splits;
   return ceil_div(ceil_div(N, 32), splits) * splits;
 }
 bool stream_plan_ok(int layout, int64_t M, int64_t N, int64_t K, const StreamShape& s) {
+  if (s.resident) return resident_shape_ok(s.resident, layout, M, N, K) && stream_splits(s, K) == 1;
   if (s.direct) return decode_shape_ok(s.direct, layout, M, N, K);
   if ((layout != kLayoutNK && layout != kLayoutP) || M > 16 * s.mt || K % s.kw != 0) return false;
   const int64_t splits = stream_splits(s, K);
@@ -174,10 +177,13 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
     // 2 <= M <= 8 with [N,K/2]: the decode kernel with the activations in LDS
     // (variant 8) before those (M = 8: 11.8 / 39.4 us against 12.3 / 41.0 us
     // whole-K; at M = 1 the whole-K kernel is faster, 10.4 against 11.1 us).
-    static const int kPrefer1[] = {6, 5, 3, 0, 1}, kPrefer8[] = {8, 6, 5, 3, 0, 1}, kPrefer16[] = {3, 0, 1},
+    // M == 1 with [N,K/2] and K % 512 == 0, K <= 8192: the resident kernel
+    // (variant 9) before those (N = 8192 / 28672, K = 8192: 10.0 / 26.9 us
+    // against 10.4 / 33.6 us whole-K).
+    static const int kPrefer1[] = {9, 6, 5, 3, 0, 1}, kPrefer8[] = {8, 6, 5, 3, 0, 1}, kPrefer16[] = {3, 0, 1},
                      kPrefer32[] = {4, 2};
     const int* pref = two ? kPrefer32 : M == 1 ? kPrefer1 : M <= 8 ? kPrefer8 : kPrefer16;
-    const int npref = two ? 2 : M == 1 ? 5 : M <= 8 ? 6 : 3;
+    const int npref = two ? 2 : M == 1 ? 6 : M <= 8 ? 6 : 3;
     for (int i = 0; i < npref; ++i) {
       const StreamShape& st = kStream[pref[i]];
       if (stream_plan_ok(layout, M, N, K, st) && stream_ctas(st, N, K) >= 192) {
@@ -619,7 +625,9 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
     case MXFP4_KERNEL_STREAM: {
       if (plan->variant < 0 || plan->variant >= kNumStream) return hipErrorInvalidValue;
       const StreamShape& s = kStream[plan->variant];
-      if (s.direct)
+      if (s.resident)
+        snprintf(buf, buf_len, "resident rows%d cols%d split%d", s.resident, 16 * s.gcb, plan->split_k);
+      else if (s.direct)
         snprintf(buf, buf_len, "decode rows%d cols%d kr%d split%d", s.direct, 16 * s.gcb, s.k_split(),
                  plan->split_k);
       else if (s.nslot == 1 && s.smax == 1)

@@ -1,5 +1,8 @@
-// Decode kernel for M <= 16 with [N, K/2] weights: activations resident in
-// LDS, weights streamed straight into VGPRs by separate waves.
+// Decode kernels with [N, K/2] weights.  The decode kernel (M <= 16):
+// activations resident in LDS, weights streamed straight into VGPRs by
+// separate waves.  The resident kernel (M <= 8, production for M = 1; its
+// notes are at its definition): every weight byte of a CTA loaded into VGPRs
+// at entry.
 //
 // The reference has no kernel for these shapes (every launcher rejects
 // M % 64 != 0, csrc/common.h:80-99).  A decode GEMM is a read of the weights
@@ -339,7 +342,133 @@ __global__ void __launch_bounds__(1024, 1) decode_kernel(StreamArgs p) {
 using Dec16 = DecodeCfg<16, 64, 4096>;  // M <= 16: 64 columns x 4096 K per CTA
 using Dec8 = DecodeCfg<8, 32, 8192>;    // M <= 8: 32 columns x 8192 K per CTA
 
+// ---- resident kernel: every weight byte of the CTA in flight at entry ------
+// One CTA of K / 512 waves per 32 columns x the whole K (K <= 8192, no split,
+// no workspace).  Wave w owns K range 512w .. 512w+511.  At entry it issues,
+// as plain global loads straight into VGPRs: its MR activation rows (1 KB
+// each, contiguous), its 2 x 16 scale bytes and its 8 weight loads (16
+// columns x 64 contiguous bytes per load, the MFMA operand order: 32
+// VGPRs) -- nothing else is in its way, and the loads return in issue order.
+// Measured on MI355X (N = K = 8192, graph-replayed, weights rotated past the
+// MALL): the weight read alone in this pattern takes 7.9 us (4.3 TB/s); the
+// whole kernel 9.6 us at M = 1 against 10.4 us for the whole-K streaming
+// kernel (scale loads +0.3 us, activations +0.2 us, the wave reduction
+// +0.1 us).  Non-temporal loads were slower here (10.0 us).  With more rows
+// the activation bytes per CU grow (M = 8: 128 KB, 11.9 us -- the decode
+// kernel above takes 11.7 us), so the auto plan uses it at M = 1.
+// * K order: load j = (ct, jj) of lane (c, q) holds bytes 64jj + 16q .. +15
+//   of the wave's 256-byte segment of column 16ct + c: K 512w + 128jj + 32q
+//   + 0..31.  MFMA (jj, s) takes word s (K .. + 8s .. +7) against activation
+//   chunk 16jj + 4q + s of row c; its scale is group 16w + 4jj + q, byte q of
+//   word jj of the lane's 16 scale bytes.
+// * Activations: the wave writes its rows to its own LDS slice (chunk j of
+//   row r at j ^ r: a 16-lane operand read hits 8 distinct 16-byte slots)
+//   and reads the MFMA operands back; only lanes with c < M read (the others
+//   give zeros).
+// * The waves' partial tiles are summed in wave order (bit-reproducible) and
+//   stored with the fused epilogue.  Columns past N load column N - 1 and are
+//   not stored.
+template <int MR>
+__global__ void __launch_bounds__(1024, 1) resident_kernel(StreamArgs p) {
+  static_assert(MR == 1 || MR == 8, "activation rows");
+  __shared__ __attribute__((aligned(16))) uint8_t alds[16 * MR * 1024];
+  __shared__ __attribute__((aligned(16))) float red[16][MR * 32];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = (int)(blockDim.x >> 6);
+  const int c = lane & 15, q = lane >> 4;
+  const int M = p.M, N = p.N, K = p.K;
+  const int col0 = 32 * (int)blockIdx.x;
+  const size_t Kh = (size_t)(K >> 1), G = (size_t)(K >> 5);
+
+  // No branch ahead of the loads: rows past M load row M - 1 and are zeroed once
+  // landed, and row 0 (M >= 1) is never selected (a branch on M made the
+  // first load wait for a second round trip of kernel-argument loads, 10.3
+  // against 9.6 us at M = 1, or sank a load below the others and drained
+  // them all before the first MFMA).
+  u32x4 av[MR];
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+    av[r] = *reinterpret_cast<const u32x4*>(p.A + (size_t)min(r, M - 1) * K + 512 * w + 8 * lane);
+  int cc[2];
+  u32x4 sv[2];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    cc[ct] = min(col0 + 16 * ct + c, N - 1);
+    sv[ct] = *reinterpret_cast<const u32x4*>(p.S + (size_t)cc[ct] * G + 16 * w);
+  }
+  u32x4 wv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    wv[j] = *reinterpret_cast<const u32x4*>(p.B + (size_t)cc[j >> 2] * Kh + 256 * w + 64 * (j & 3) + 16 * q);
+
+  // slots of waves this CTA does not have (K < 8192) add zeros in the reduction
+  for (int i = (int)threadIdx.x; i < (16 - nw) * MR * 32; i += (int)blockDim.x) red[nw + i / (MR * 32)][i % (MR * 32)] = 0.f;
+
+  uint8_t* const my = alds + w * MR * 1024;
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+    *reinterpret_cast<u32x4*>(my + r * 1024 + 16 * (lane ^ r)) = (r == 0 || r < M) ? av[r] : u32x4{0u, 0u, 0u, 0u};
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave reads only its own slice
+  __builtin_amdgcn_wave_barrier();
+
+  const int rc = c < MR ? c : 0;
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int ct = j >> 2, jj = j & 3;
+    const float f = e8m0_to_f32((sv[ct][jj] >> (8 * q)) & 0xFFu);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const bf16x8 b = operand_from_word(wv[j][s], f);
+      const int ch = 16 * jj + 4 * q + s;
+      u32x4 a = u32x4{0u, 0u, 0u, 0u};
+      if (c < M && c < MR) a = *reinterpret_cast<const u32x4*>(my + rc * 1024 + 16 * (ch ^ rc));
+      acc[ct] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a), b, acc[ct]);
+    }
+  }
+  // D lane (c, q) holds rows 4q .. 4q+3 of column c
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * q + i < MR) red[w][(4 * q + i) * 32 + 16 * ct + c] = acc[ct][i];
+  __syncthreads();
+  for (int e = threadIdx.x; e < MR * 32; e += blockDim.x) {
+    const int row = e >> 5, col = col0 + (e & 31);
+    if (row >= M || col >= N) continue;
+    // all 16 slots read at once and added in wave order (slots past nw hold
+    // zeros): a loop bounded by nw issued the reads one round trip at a time,
+    // and per-slot conditions cost 22 SGPRs (two CTAs per CU no longer fit)
+    float x = red[0][e];
+#pragma unroll
+    for (int ww = 1; ww < 16; ++ww) x += red[ww][e];
+    const float y = p.ep.any ? epilogue_value(p.ep, x, row, col, N) : x;
+    if (p.out_bf16)
+      static_cast<uint16_t*>(p.C)[(size_t)row * N + col] = (uint16_t)bf16_bits_rne(y);
+    else
+      static_cast<float*>(p.C)[(size_t)row * N + col] = y;
+  }
+}
+
 }  // namespace
+
+// Resident kernel shape rules: [N,K/2], 1 <= M <= rows (1 or 8), K a multiple
+// of 512 up to 8192 (K / 512 waves of 64 lanes).
+bool resident_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K) {
+  return (rows == 1 || rows == 8) && layout == kLayoutNK && M >= 1 && M <= rows && N >= 1 && K >= 512 &&
+         K <= 8192 && K % 512 == 0;
+}
+
+hipError_t launch_resident(int rows, int layout, const StreamArgs& a, hipStream_t stream) {
+  if (!resident_shape_ok(rows, layout, a.M, a.N, a.K) || a.splits != 1) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((a.N + 31) / 32)), block((unsigned)(a.K / 512 * 64));
+  if (rows == 1)
+    hipLaunchKernelGGL(resident_kernel<1>, grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL(resident_kernel<8>, grid, block, 0, stream, a);
+  return hipGetLastError();
+}
 
 int64_t decode_splits(int rows, int64_t K) {
   const int64_t kr = rows <= 8 ? 8192 : 4096;

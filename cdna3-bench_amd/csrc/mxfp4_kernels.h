@@ -124,7 +124,8 @@ struct StreamShape {
   int nslot;  // LDS ring units per wave
   int smax;   // largest split count of this instantiation
   int kw;     // K per compute wave and unit (256 or 512)
-  int direct = 0;  // 8 or 16: the decode kernel (mxfp4_decode.hip) for M <= direct
+  int direct = 0;    // 8 or 16: the decode kernel (mxfp4_decode.hip) for M <= direct
+  int resident = 0;  // 1 or 8: the resident kernel (mxfp4_decode.hip) for M <= resident
   int k_split() const { return waves * kw; }
   int tile() const { return 16 * mt * 16 * gcb; }
 };
@@ -141,6 +142,13 @@ int64_t decode_splits(int rows, int64_t K);
 size_t decode_workspace(int rows, int64_t N, int64_t K);
 bool decode_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K);
 hipError_t launch_decode(int rows, int layout, const StreamArgs& args, hipStream_t stream);
+
+// Resident kernel (mxfp4_decode.hip): [N,K/2], M <= rows with rows = 1 or 8,
+// one CTA of K / 512 waves per 32 columns x the whole K (K % 512 == 0,
+// K <= 8192), every weight load issued at entry into VGPRs; no split, no
+// workspace.
+bool resident_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K);
+hipError_t launch_resident(int rows, int layout, const StreamArgs& args, hipStream_t stream);
 
 // Any shape with K % 32 == 0; one thread per output, for shapes the fast
 // families do not cover (N % 16 != 0, unaligned pointers).

@@ -791,6 +791,9 @@ bool whole_shape(const StreamShape& s) {
 }
 
 bool stream_shape_available(const StreamShape& s) {
+  if (s.resident)
+    return s.mt == 1 && s.waves == 16 && s.gcb == 2 && s.nslot == 0 && s.smax == 1 && s.kw == 512 &&
+           s.direct == 0 && (s.resident == 1 || s.resident == 8);
   if (s.direct)
     return s.mt == 1 && s.waves == 8 && s.nslot == 0 && s.smax == 8 &&
            ((s.direct == 16 && s.gcb == 4 && s.kw == 512) || (s.direct == 8 && s.gcb == 2 && s.kw == 1024));
@@ -804,6 +807,7 @@ bool stream_shape_available(const StreamShape& s) {
 }
 
 hipError_t launch_stream(int layout, const StreamShape& s, const StreamArgs& args, hipStream_t stream) {
+  if (s.resident) return launch_resident(s.resident, layout, args, stream);
   if (s.direct) return launch_decode(s.direct, layout, args, stream);
   if (whole_shape(s)) {
     if (args.splits != 1) return hipErrorInvalidValue;

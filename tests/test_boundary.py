@@ -189,7 +189,11 @@ def test_plan_from_python(kk):
     kind, _, split, desc = kk.select_plan(8, 8192, 8192, "nk")
     assert kind == kk.KERNEL_STREAM and desc.startswith("decode rows8") and split == 1
     kind, _, split, desc = kk.select_plan(1, 8192, 8192, "nk")
-    assert kind == kk.KERNEL_STREAM and desc.startswith("stream-whole") and split == 1
+    assert kind == kk.KERNEL_STREAM and desc.startswith("resident rows1") and split == 1
+    kind, _, split, desc = kk.select_plan(1, 28672, 8192, "nk")
+    assert kind == kk.KERNEL_STREAM and desc.startswith("resident rows1") and split == 1
+    desc = kk.select_plan(1, 8192, 12288, "nk")[3]  # K > 8192: not the resident kernel
+    assert not desc.startswith("resident"), desc
     kind, _, split, desc = kk.select_plan(8, 8192, 8192, "p")
     assert kind == kk.KERNEL_STREAM and desc.startswith("stream-whole") and split == 1
     kind, _, _, desc = kk.select_plan(16, 8192, 8192, "kn")

@@ -373,6 +373,44 @@ def test_decode_rejects(kk, variant, rows, kr, kg):
             run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=(kk.KERNEL_STREAM, variant, split))
 
 
+# resident kernel variants: (variant, rows)
+RESIDENT_VARIANTS = [(9, 1), (10, 8)]
+
+
+@pytest.mark.parametrize("variant,rows", RESIDENT_VARIANTS)
+def test_resident_variants(kk, variant, rows):
+    """Resident kernel ([N,K/2], M <= rows, K % 512 == 0, K <= 8192): one wave
+    (K = 512) up to 16 waves (K = 8192), ragged M, N % 32 != 0 and odd N,
+    fp32 and bf16 out; repeat calls are bitwise identical and bf16 out is
+    the fp32 result rounded."""
+    import torch
+
+    for M in sorted({1, min(5, rows), rows}):
+        for N, K in ((512, 512), (1000, 1536), (1001, 4096), (4096, 8192), (96, 8192), (33, 2560)):
+            log(f"case resident variant={variant} M={M} N={N} K={K}")
+            A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=M + N + K + 13)
+            ref = oracle_f64(A_bits, W, S)
+            plan = (kk.KERNEL_STREAM, variant, 1)
+            out = run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan)
+            bad = mo.strict_violations(out, ref, K)
+            assert bad == 0, f"M={M} N={N} K={K}: {bad} bad"
+            again = run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan)
+            assert np.array_equal(out, again), f"M={M} N={N} K={K}: not deterministic"
+            out16 = run_gemm(kk, A_bits, W, S, "nk", torch.bfloat16, plan=plan)
+            assert np.array_equal(out16, mo.bf16_bits_to_f32(mo.f32_to_bf16_bits(out))), f"M={M} N={N} K={K}"
+
+
+@pytest.mark.parametrize("variant,rows", RESIDENT_VARIANTS)
+def test_resident_rejects(kk, variant, rows):
+    import torch
+
+    for M, K, layout, split in ((rows + 1, 512, "nk", 1), (rows, 8704, "nk", 1), (rows, 8704, "nk", 2),
+                                (rows, 768, "nk", 1), (rows, 512, "p", 1), (rows, 512, "kn", 1), (rows, 512, "nk", 2)):
+        A_bits, W, S = mo.make_inputs(M, 64, K, 120, 132, seed=4)
+        with pytest.raises(RuntimeError, match="invalid argument"):  # M, K > 8192, K % 512, layout, split count
+            run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=(kk.KERNEL_STREAM, variant, split))
+
+
 @pytest.mark.parametrize("M", [24, 32])
 def test_wide_nk_decode_takes_gemv(kk, M):
     """[N,K/2], 16 < M <= 32, N >= 16384: the auto plan is the GEMV family
