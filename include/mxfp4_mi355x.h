@@ -56,7 +56,9 @@ enum {
   MXFP4_KERNEL_TILED = 2,   /* MFMA-bound tiled family */
   MXFP4_KERNEL_GENERIC = 3, /* one thread per output, any N */
   MXFP4_KERNEL_STREAM = 4   /* weight streaming, M <= 32, NK or P layout, K % 256 == 0: split-K
-                               (variants 0-4) and whole-K (5, 6: M <= 16) kernels */
+                               (variants 0-4) and whole-K (5, 6: M <= 16) kernels; NK only:
+                               decode (7: M <= 16, 8: M <= 8) and resident (9: M == 1,
+                               10: M <= 8; K % 512 == 0, K <= 8192) kernels */
 };
 
 /* A launch plan: which kernel family, which tile variant, how many K splits. */
