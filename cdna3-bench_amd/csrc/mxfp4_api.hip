@@ -97,6 +97,7 @@ const StreamShape kStream[] = {
     {1, 8, 2, 0, 8, 1024, 8},  // 8: decode kernel, M <= 8, [N,K/2], 32 columns x 8192 K per CTA, K % 1024 == 0
     {1, 16, 2, 0, 1, 512, 0, 1},  // 9: resident kernel, M == 1, [N,K/2], 32 columns x K <= 8192 per CTA, K % 512 == 0
     {1, 16, 2, 0, 1, 512, 0, 8},  // 10: resident kernel, M <= 8 (explicit plans only)
+    {2, 8, 8, 0, 8, 256, 0, 32},  // 11: resident split kernel, M <= 32, [N,K/2], 128 columns x 2048 K per CTA, K % 256 == 0
 };
 constexpr int kNumStream = sizeof(kStream) / sizeof(kStream[0]);
 constexpr int kStreamSpin = 4096;  // late-unit polls before counter arbitration
@@ -125,7 +126,7 @@ int64_t stream_ctas(const StreamShape& s, int64_t N, int64_t K) {
   return ceil_div(ceil_div(N, 32), splits) * splits;
 }
 bool stream_plan_ok(int layout, int64_t M, int64_t N, int64_t K, const StreamShape& s) {
-  if (s.resident) return resident_shape_ok(s.resident, layout, M, N, K) && stream_splits(s, K) == 1;
+  if (s.resident) return resident_shape_ok(s.resident, layout, M, N, K) && stream_splits(s, K) == resident_splits(s.resident, K);
   if (s.direct) return decode_shape_ok(s.direct, layout, M, N, K);
   if ((layout != kLayoutNK && layout != kLayoutP) || M > 16 * s.mt || K % s.kw != 0) return false;
   const int64_t splits = stream_splits(s, K);
@@ -157,6 +158,18 @@ void choose_tiled(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out, 
 // weight bytes, so S stays small.
 void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
   const bool two = M > 16;
+  // 16 < M <= 32 with [N,K/2]: the resident split kernel (variant 11: 128
+  // columns x 2048 K per CTA, the weights converted once for 32 rows) first,
+  // at any N (K = 8192, M = 17 / 32: 15.3 / 16.2 us at N = 8192 against 21.0
+  // / 21.3 us streaming; 28.3 / 30.0 us at N = 16384 against 35.1 / 37.2 us
+  // for the GEMV family below).
+  if (two && layout == kLayoutNK) {
+    const StreamShape& st = kStream[11];
+    if (stream_plan_ok(layout, M, N, K, st) && stream_ctas(st, N, K) >= 192) {
+      *out = {MXFP4_KERNEL_STREAM, 11, (int32_t)stream_splits(st, K), 0};
+      return;
+    }
+  }
   // [N,K/2] with enough column groups to fill the chip: the streaming split-K
   // kernel, first choice that fits (measured on MI355X at N = 8192 / 28672,
   // K = 8192: 512-K waves with 2 splits beat 256-K waves with 4; both beat
@@ -386,7 +399,9 @@ size_t split_workspace(int layout, int64_t M, int64_t N, int64_t K, const mxfp4_
   } else if (p.kernel == MXFP4_KERNEL_STREAM) {
     const StreamShape& s = kStream[p.variant];
     // 8-byte (value, tag) packets per partial element
-    partial = s.direct ? decode_workspace(s.direct, N, K) : (size_t)stream_ctas(s, N, K) * p.split_k * s.tile() * 8;
+    partial = s.resident ? resident_workspace(s.resident, N, K)
+              : s.direct ? decode_workspace(s.direct, N, K)
+                         : (size_t)stream_ctas(s, N, K) * p.split_k * s.tile() * 8;
   } else if (p.kernel == MXFP4_KERNEL_TILED) {
     const TiledShape& s = kTiled[p.variant].shape;
     const int64_t ksteps = ceil_div(K, 64);
@@ -625,7 +640,10 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
     case MXFP4_KERNEL_STREAM: {
       if (plan->variant < 0 || plan->variant >= kNumStream) return hipErrorInvalidValue;
       const StreamShape& s = kStream[plan->variant];
-      if (s.resident)
+      if (s.resident == 32)
+        snprintf(buf, buf_len, "resident rows%d cols%d kr%d split%d", s.resident, 16 * s.gcb, s.k_split(),
+                 plan->split_k);
+      else if (s.resident)
         snprintf(buf, buf_len, "resident rows%d cols%d split%d", s.resident, 16 * s.gcb, plan->split_k);
       else if (s.direct)
         snprintf(buf, buf_len, "decode rows%d cols%d kr%d split%d", s.direct, 16 * s.gcb, s.k_split(),

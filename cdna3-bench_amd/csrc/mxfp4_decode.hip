@@ -451,17 +451,217 @@ __global__ void __launch_bounds__(1024, 1) resident_kernel(StreamArgs p) {
   }
 }
 
+// ---- resident split kernel: 17 <= M <= 32 ------------------------------------
+// One CTA of 8 waves per 128 columns x 2048 K (S = ceil(K / 2048) CTAs per
+// column group); wave w owns K 256w .. 256w+255 of the CTA's range.  At entry
+// every wave issues its 32 activation rows (16 loads of 1 KB: 2 rows x 512 B
+// each), 8 x 8 scale bytes and 16 weight loads in the MFMA operand order (8
+// column blocks x 2 halves of 128 K: 64 VGPRs), all straight into VGPRs.
+// The activations go to the wave's own LDS slice (chunk j of row r at
+// j ^ (r & 7)); both 16-row halves run against the same weight registers,
+// so the weights are converted once for 32 rows.  Measured on MI355X (N = K
+// = 8192, M = 32, graph-replayed): 14.6 us for the kernel body against
+// 21.2 us for the split-K streaming kernel, whose 8-byte packets for 4
+// splits of 32-column units wrote 25 MB per launch.
+// * K order: half h, word s of lane (c, q) holds K k0 + 128h + 32q + 8s .. +7
+//   of column 16cb + c (k0 = the wave's first K); activation chunk
+//   16h + 4q + s of the wave's slice; scale group 4h + q, byte q of word h
+//   of the lane's 8 scale bytes.
+// * The 8 wave tiles (32 x 128 fp32) are summed in wave order through the
+//   LDS (the activation slices are dead by then); thread t owns elements
+//   4t .. 4t+3 and 2048 + 4t .. +3.  K splits meet as plain fp32 partials
+//   summed in split order by the last arrival on the group counter (no
+//   polling, so nothing assumes the CTAs are co-resident; bit-reproducible).
+// * Waves whose K range is past K load the last range and zero their
+//   weights; columns past N load column N-1 and are not stored; rows past M
+//   load row M-1 and their operands are zeroed when read back (a condition
+//   on the stored value let the compiler sink a load below the others and
+//   drain them all first).
+constexpr int kRsCols = 128, kRsKr = 2048, kRsWaves = 8, kRsTile = 32 * kRsCols;
+
+__global__ void __launch_bounds__(512, 1) resident_split_kernel(StreamArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kRsWaves * 16384];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, q = lane >> 4;
+  const int S = p.splits;
+  const int r = (int)blockIdx.x % S, g = (int)blockIdx.x / S;
+  const int M = p.M, N = p.N, K = p.K;
+  const size_t Kh = (size_t)(K >> 1), G = (size_t)(K >> 5);
+  const int k0 = r * kRsKr + 256 * w;
+  const bool kok = k0 < K;  // K % 256 == 0: a wave's range is all in or all out
+  const int kl = kok ? k0 : K - 256;
+  const int col0 = kRsCols * g;
+
+  u32x4 av[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = min(2 * i + (lane >> 5), M - 1);
+    av[i] = *reinterpret_cast<const u32x4*>(p.A + (size_t)row * K + kl + 8 * (lane & 31));
+  }
+  u32x2 sv[8];
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb)
+    sv[cb] = *reinterpret_cast<const u32x2*>(p.S + (size_t)min(col0 + 16 * cb + c, N - 1) * G + kl / 32);
+  u32x4 wv[8][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb)
+      wv[cb][h] = *reinterpret_cast<const u32x4*>(p.B + (size_t)min(col0 + 16 * cb + c, N - 1) * Kh + kl / 2 +
+                                                  64 * h + 16 * q);
+
+  uint8_t* const my = smem + w * 16384;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = 2 * i + (lane >> 5), ch = lane & 31;
+    *reinterpret_cast<u32x4*>(my + row * 512 + 16 * (ch ^ (row & 7))) = av[i];
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave reads only its own slice
+  __builtin_amdgcn_wave_barrier();
+
+  f32x4 acc[2][8];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) acc[mt][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int ch = 16 * h + 4 * q + s;
+      u32x4 a0 = *reinterpret_cast<const u32x4*>(my + c * 512 + 16 * (ch ^ (c & 7)));
+      u32x4 a1 = *reinterpret_cast<const u32x4*>(my + (16 + c) * 512 + 16 * (ch ^ (c & 7)));
+      if (c >= M) a0 = u32x4{0u, 0u, 0u, 0u};
+      if (16 + c >= M) a1 = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) {
+        // a wave past K multiplies zero codes by 2^0 (its loaded scales may be 0xFF: NaN)
+        const float f = e8m0_to_f32(kok ? (sv[cb][h] >> (8 * q)) & 0xFFu : 127u);
+        const bf16x8 b = operand_from_word(kok ? wv[cb][h][s] : 0u, f);
+        acc[0][cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a0), b, acc[0][cb]);
+        acc[1][cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a1), b, acc[1][cb]);
+      }
+    }
+  __syncthreads();  // every wave has read its activations: the LDS now takes the tiles
+  float* const part = reinterpret_cast<float*>(smem) + w * kRsTile;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[(16 * mt + 4 * q + i) * kRsCols + 16 * cb + c] = acc[mt][cb][i];
+  __syncthreads();
+
+  // the CTA's sum in wave order: thread t owns elements 4t .. 4t+3 (v = 0)
+  // and 2048 + 4t .. +3 (v = 1)
+  f32x4 own[2];
+#pragma unroll
+  for (int v = 0; v < 2; ++v) {
+    const float* src = reinterpret_cast<const float*>(smem) + 2048 * v + 4 * tid;
+    own[v] = *reinterpret_cast<const f32x4*>(src);
+#pragma unroll
+    for (int ww = 1; ww < kRsWaves; ++ww) own[v] += *reinterpret_cast<const f32x4*>(src + ww * kRsTile);
+  }
+  auto store_c = [&](const f32x4 (&x)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int e = 2048 * v + 4 * tid;
+      const int row = e / kRsCols, col = col0 + e % kRsCols;
+      if (row >= M) continue;
+      float y[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = p.ep.any ? epilogue_value(p.ep, x[v][i], row, col + i, N) : x[v][i];
+      if (p.out_bf16) {
+        uint16_t* out = static_cast<uint16_t*>(p.C) + (size_t)row * N + col;
+        if ((N & 3) == 0 && col + 3 < N) {
+          *reinterpret_cast<u32x2*>(out) = u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (col + i < N) out[i] = (uint16_t)bf16_bits_rne(y[i]);
+        }
+      } else {
+        float* out = static_cast<float*>(p.C) + (size_t)row * N + col;
+        if ((N & 3) == 0 && col + 3 < N) {
+          *reinterpret_cast<f32x4*>(out) = f32x4{y[0], y[1], y[2], y[3]};
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (col + i < N) out[i] = y[i];
+        }
+      }
+    }
+  };
+  if (S == 1) {
+    store_c(own);
+    return;
+  }
+
+  // ---- split-K across the group's S CTAs ----
+  // Plain fp32 partials (rows < M) with device-coherent stores; the last of
+  // the S arrivals on the group counter sums the splits in split order (its
+  // own from registers, every other split's loads in flight together) and
+  // resets the counter.  Tagged packets (8 bytes per value, cleared after
+  // use) cost 23.2 us here at M = 32: 19 MB of packet traffic per launch.
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.partials + (size_t)g * S * kRsTile);
+  bool live[2];
+#pragma unroll
+  for (int v = 0; v < 2; ++v) {
+    live[v] = (2048 * v + 4 * tid) / kRsCols < M;
+    if (live[v]) store_coherent(rp, (uint32_t)((r * kRsTile + 2048 * v + 4 * tid) * 4), own[v]);
+  }
+  if (!splitk_arrive_last(p.counters + g, (uint32_t)S, &s_last, tid)) return;
+  f32x4 t[8][2];
+#pragma unroll
+  for (int sp = 0; sp < 8; ++sp)
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+      t[sp][v] = sp < S && sp != r && live[v] ? load_coherent4(rp, (uint32_t)((sp * kRsTile + 2048 * v + 4 * tid) * 4))
+                                              : own[v];
+  f32x4 tot[2] = {t[0][0], t[0][1]};
+#pragma unroll
+  for (int sp = 1; sp < 8; ++sp)
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+      if (sp < S) tot[v] += t[sp][v];
+  store_c(tot);
+}
+
 }  // namespace
 
-// Resident kernel shape rules: [N,K/2], 1 <= M <= rows (1 or 8), K a multiple
-// of 512 up to 8192 (K / 512 waves of 64 lanes).
+int64_t resident_splits(int rows, int64_t K) { return rows == 32 ? (K + kRsKr - 1) / kRsKr : 1; }
+int64_t resident_groups(int rows, int64_t N) {
+  const int64_t cw = rows == 32 ? kRsCols : 32;
+  return (N + cw - 1) / cw;
+}
+size_t resident_workspace(int rows, int64_t N, int64_t K) {
+  const int64_t S = resident_splits(rows, K);
+  return S > 1 ? (size_t)(resident_groups(rows, N) * S * kRsTile * 4) : 0;
+}
+
+// Resident kernel shape rules: [N,K/2], 1 <= M <= rows.  rows 1 or 8: K a
+// multiple of 512 up to 8192 (K / 512 waves of 64 lanes, no split).  rows 32:
+// K a multiple of 256, at most 8 splits of 2048, one counter per 128-column
+// group and the partials within 1 GiB.
 bool resident_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K) {
-  return (rows == 1 || rows == 8) && layout == kLayoutNK && M >= 1 && M <= rows && N >= 1 && K >= 512 &&
-         K <= 8192 && K % 512 == 0;
+  if (layout != kLayoutNK || M < 1 || M > rows || N < 1) return false;
+  if (rows == 1 || rows == 8) return K >= 512 && K <= 8192 && K % 512 == 0;
+  return rows == 32 && K >= 256 && K % 256 == 0 && resident_splits(rows, K) <= 8 &&
+         resident_groups(rows, N) * 4 <= (int64_t)MXFP4_COUNTER_BYTES &&
+         resident_workspace(rows, N, K) <= (size_t)kNumRecords;
 }
 
 hipError_t launch_resident(int rows, int layout, const StreamArgs& a, hipStream_t stream) {
-  if (!resident_shape_ok(rows, layout, a.M, a.N, a.K) || a.splits != 1) return hipErrorInvalidValue;
+  if (!resident_shape_ok(rows, layout, a.M, a.N, a.K) || a.splits != resident_splits(rows, a.K))
+    return hipErrorInvalidValue;
+  if (rows == 32) {
+    if (a.splits > 1 && (!a.partials || !a.counters)) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)(resident_groups(rows, a.N) * a.splits);
+    hipLaunchKernelGGL(resident_split_kernel, dim3(grid), dim3(64 * kRsWaves), 0, stream, a);
+    return hipGetLastError();
+  }
   const dim3 grid((unsigned)((a.N + 31) / 32)), block((unsigned)(a.K / 512 * 64));
   if (rows == 1)
     hipLaunchKernelGGL(resident_kernel<1>, grid, block, 0, stream, a);

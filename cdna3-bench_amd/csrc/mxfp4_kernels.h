@@ -125,7 +125,7 @@ struct StreamShape {
   int smax;   // largest split count of this instantiation
   int kw;     // K per compute wave and unit (256 or 512)
   int direct = 0;    // 8 or 16: the decode kernel (mxfp4_decode.hip) for M <= direct
-  int resident = 0;  // 1 or 8: the resident kernel (mxfp4_decode.hip) for M <= resident
+  int resident = 0;  // 1, 8 or 32: a resident kernel (mxfp4_decode.hip) for M <= resident
   int k_split() const { return waves * kw; }
   int tile() const { return 16 * mt * 16 * gcb; }
 };
@@ -143,10 +143,14 @@ size_t decode_workspace(int rows, int64_t N, int64_t K);
 bool decode_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K);
 hipError_t launch_decode(int rows, int layout, const StreamArgs& args, hipStream_t stream);
 
-// Resident kernel (mxfp4_decode.hip): [N,K/2], M <= rows with rows = 1 or 8,
-// one CTA of K / 512 waves per 32 columns x the whole K (K % 512 == 0,
-// K <= 8192), every weight load issued at entry into VGPRs; no split, no
-// workspace.
+// Resident kernels (mxfp4_decode.hip): [N,K/2], every weight load of a CTA
+// issued at entry into VGPRs.  rows = 1 or 8 (M <= rows): one CTA of K / 512
+// waves per 32 columns x the whole K (K % 512 == 0, K <= 8192), no split, no
+// workspace.  rows = 32 (M <= 32): one CTA of 8 waves per 128 columns x 2048
+// K, S = ceil(K / 2048) <= 8 CTAs per column group whose fp32 partials
+// (resident_workspace bytes after the counters) the last arrival sums.
+int64_t resident_splits(int rows, int64_t K);
+size_t resident_workspace(int rows, int64_t N, int64_t K);
 bool resident_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K);
 hipError_t launch_resident(int rows, int layout, const StreamArgs& args, hipStream_t stream);
 

@@ -103,6 +103,8 @@ def test_stream_counter_path_matches_poll_path(lib, M, layout):
     A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(Bl), to_dev_u8(Sl)
     plan = Plan()
     assert lib.mxfp4_select_plan(M, N, K, LAYOUT[layout], ctypes.byref(plan)) == 0
+    if (plan.kernel, plan.variant) == (4, 11):
+        plan = Plan(4, 4, 4, 0)  # M > 16 on [N,K/2] auto-selects the resident split kernel; test the streaming one
     assert plan.kernel == 4 and plan.split_k > 1, "decode plan is the streaming split-K kernel"
     wsb = lib.mxfp4_gemm_workspace_bytes(M, N, K, LAYOUT[layout], ctypes.byref(plan))
     ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
@@ -124,6 +126,39 @@ def test_stream_counter_path_matches_poll_path(lib, M, layout):
     cols = np.random.default_rng(0).choice(N, 512, replace=False)
     ref = oracle_f64(A_bits, W, S, rows, cols)
     assert mo.strict_violations(outs[1][:, cols], ref, K) == 0
+
+
+@pytest.mark.parametrize("M,K", [(32, 8192), (21, 16384 - 256)])
+def test_resident_split_counters_return_to_zero(lib, M, K):
+    """The resident split kernel (variant 11) through mxfp4_gemm_with_plan:
+    its fp32 partials stay in the workspace, its group counters are zero
+    after every call, and repeated calls on the same workspace are bitwise
+    identical and within the tolerance of the oracle."""
+    import torch
+
+    N = 4096
+    log(f"case resident split counters M={M} K={K}")
+    A_bits, W, S = mo.make_inputs(M, N, K, 122, 130, 1.0, seed=M + K)
+    A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(W), to_dev_u8(S)
+    plan = Plan(4, 11, -(-K // 2048), 0)
+    assert plan.split_k > 1
+    wsb = lib.mxfp4_gemm_workspace_bytes(M, N, K, LAYOUT["nk"], ctypes.byref(plan))
+    assert wsb == COUNTER_BYTES + -(-(N // 128) * plan.split_k * 32 * 128 * 4 // 256) * 256
+    ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
+    outs = []
+    for _ in range(3):
+        C = torch.empty(M, N, dtype=torch.float32, device="cuda")
+        err = lib.mxfp4_gemm_with_plan(A.data_ptr(), B.data_ptr(), Sd.data_ptr(), C.data_ptr(), 0,
+                                       M, N, K, LAYOUT["nk"], ctypes.byref(plan), ws.data_ptr(), wsb, _stream())
+        assert err == 0
+        torch.cuda.synchronize()
+        assert ws[:COUNTER_BYTES].count_nonzero().item() == 0, "counters not reset"
+        outs.append(C.cpu().numpy())
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    cols = np.random.default_rng(2).choice(N, 256, replace=False)
+    ref = oracle_f64(A_bits, W, S, np.arange(M), cols)
+    assert mo.strict_violations(outs[0][:, cols], ref, K) == 0
 
 
 @pytest.mark.parametrize("variant,M,K", [(7, 16, 8192), (8, 8, 16384), (7, 13, 12800)])
