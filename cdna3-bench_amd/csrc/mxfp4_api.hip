@@ -100,6 +100,7 @@ const StreamShape kStream[] = {
     {1, 16, 2, 0, 1, 512, 0, 1},  // 9: resident kernel, M == 1, [N,K/2], 32 columns x K <= 8192 per CTA, K % 512 == 0
     {1, 16, 2, 0, 1, 512, 0, 8},  // 10: resident kernel, M <= 8 (explicit plans only)
     {2, 8, 8, 0, 8, 256, 0, 32},  // 11: resident split kernel, M <= 32, [N,K/2], 128 columns x 2048 K per CTA, K % 256 == 0
+    {1, 8, 8, 0, 8, 256, 0, 16},  // 12: resident split kernel, M <= 16, two CTAs per CU
 };
 constexpr int kNumStream = sizeof(kStream) / sizeof(kStream[0]);
 constexpr int kStreamSpin = 4096;  // late-unit polls before counter arbitration
@@ -165,10 +166,14 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
   // at any N (K = 8192, M = 17 / 32: 15.3 / 16.2 us at N = 8192 against 21.0
   // / 21.3 us streaming; 28.3 / 30.0 us at N = 16384 against 35.1 / 37.2 us
   // for the GEMV family below).
-  if (two && layout == kLayoutNK) {
-    const StreamShape& st = kStream[11];
+  // 8 < M <= 16 with [N,K/2] and N >= 16384: its 16-row form (variant 12,
+  // two CTAs per CU; K = 8192, M = 16: 23.4 / 39.5 us at N = 16384 / 28672
+  // against 24.8 / 42.2 us for the split-K streaming kernel, which stays
+  // faster at N = 8192: 12.7 against 14.7 us).
+  if ((two || (M > 8 && N >= 16384)) && layout == kLayoutNK) {
+    const StreamShape& st = kStream[two ? 11 : 12];
     if (stream_plan_ok(layout, M, N, K, st) && stream_ctas(st, N, K) >= 192) {
-      *out = {MXFP4_KERNEL_STREAM, 11, (int32_t)stream_splits(st, K), 0};
+      *out = {MXFP4_KERNEL_STREAM, two ? 11 : 12, (int32_t)stream_splits(st, K), 0};
       return;
     }
   }
@@ -642,7 +647,7 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
     case MXFP4_KERNEL_STREAM: {
       if (plan->variant < 0 || plan->variant >= kNumStream) return hipErrorInvalidValue;
       const StreamShape& s = kStream[plan->variant];
-      if (s.resident == 32)
+      if (s.resident >= 16)
         snprintf(buf, buf_len, "resident rows%d cols%d kr%d split%d", s.resident, 16 * s.gcb, s.k_split(),
                  plan->split_k);
       else if (s.resident)

@@ -477,10 +477,14 @@ __global__ void __launch_bounds__(1024, 1) resident_kernel(StreamArgs p) {
 //   load row M-1 and their operands are zeroed when read back (a condition
 //   on the stored value let the compiler sink a load below the others and
 //   drain them all first).
-constexpr int kRsCols = 128, kRsKr = 2048, kRsWaves = 8, kRsTile = 32 * kRsCols;
+constexpr int kRsCols = 128, kRsKr = 2048, kRsWaves = 8;
 
-__global__ void __launch_bounds__(512, 1) resident_split_kernel(StreamArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kRsWaves * 16384];
+// MT 16-row tiles (M <= 16 MT); MT = 1 fits two CTAs per CU (4 waves per
+// SIMD: <= 128 VGPRs; the second launch bound is waves per SIMD).
+template <int MT>
+__global__ void __launch_bounds__(512, MT == 1 ? 4 : 2) resident_split_kernel(StreamArgs p) {
+  constexpr int kRsTile = 16 * MT * kRsCols;  // floats per CTA tile
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kRsWaves * MT * 8192];
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -494,9 +498,9 @@ __global__ void __launch_bounds__(512, 1) resident_split_kernel(StreamArgs p) {
   const int kl = kok ? k0 : K - 256;
   const int col0 = kRsCols * g;
 
-  u32x4 av[16];
+  u32x4 av[8 * MT];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 8 * MT; ++i) {
     const int row = min(2 * i + (lane >> 5), M - 1);
     av[i] = *reinterpret_cast<const u32x4*>(p.A + (size_t)row * K + kl + 8 * (lane & 31));
   }
@@ -512,18 +516,18 @@ __global__ void __launch_bounds__(512, 1) resident_split_kernel(StreamArgs p) {
       wv[cb][h] = *reinterpret_cast<const u32x4*>(p.B + (size_t)min(col0 + 16 * cb + c, N - 1) * Kh + kl / 2 +
                                                   64 * h + 16 * q);
 
-  uint8_t* const my = smem + w * 16384;
+  uint8_t* const my = smem + w * MT * 8192;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 8 * MT; ++i) {
     const int row = 2 * i + (lane >> 5), ch = lane & 31;
     *reinterpret_cast<u32x4*>(my + row * 512 + 16 * (ch ^ (row & 7))) = av[i];
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave reads only its own slice
   __builtin_amdgcn_wave_barrier();
 
-  f32x4 acc[2][8];
+  f32x4 acc[MT][8];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) acc[mt][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -531,23 +535,25 @@ __global__ void __launch_bounds__(512, 1) resident_split_kernel(StreamArgs p) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int ch = 16 * h + 4 * q + s;
-      u32x4 a0 = *reinterpret_cast<const u32x4*>(my + c * 512 + 16 * (ch ^ (c & 7)));
-      u32x4 a1 = *reinterpret_cast<const u32x4*>(my + (16 + c) * 512 + 16 * (ch ^ (c & 7)));
-      if (c >= M) a0 = u32x4{0u, 0u, 0u, 0u};
-      if (16 + c >= M) a1 = u32x4{0u, 0u, 0u, 0u};
+      u32x4 a[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        a[mt] = *reinterpret_cast<const u32x4*>(my + (16 * mt + c) * 512 + 16 * (ch ^ (c & 7)));
+        if (16 * mt + c >= M) a[mt] = u32x4{0u, 0u, 0u, 0u};
+      }
 #pragma unroll
       for (int cb = 0; cb < 8; ++cb) {
         // a wave past K multiplies zero codes by 2^0 (its loaded scales may be 0xFF: NaN)
         const float f = e8m0_to_f32(kok ? (sv[cb][h] >> (8 * q)) & 0xFFu : 127u);
         const bf16x8 b = operand_from_word(kok ? wv[cb][h][s] : 0u, f);
-        acc[0][cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a0), b, acc[0][cb]);
-        acc[1][cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a1), b, acc[1][cb]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][cb] = mfma_16x16x32(__builtin_bit_cast(bf16x8, a[mt]), b, acc[mt][cb]);
       }
     }
   __syncthreads();  // every wave has read its activations: the LDS now takes the tiles
   float* const part = reinterpret_cast<float*>(smem) + w * kRsTile;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb)
 #pragma unroll
@@ -556,17 +562,17 @@ __global__ void __launch_bounds__(512, 1) resident_split_kernel(StreamArgs p) {
 
   // the CTA's sum in wave order: thread t owns elements 4t .. 4t+3 (v = 0)
   // and 2048 + 4t .. +3 (v = 1)
-  f32x4 own[2];
+  f32x4 own[MT];
 #pragma unroll
-  for (int v = 0; v < 2; ++v) {
+  for (int v = 0; v < MT; ++v) {
     const float* src = reinterpret_cast<const float*>(smem) + 2048 * v + 4 * tid;
     own[v] = *reinterpret_cast<const f32x4*>(src);
 #pragma unroll
     for (int ww = 1; ww < kRsWaves; ++ww) own[v] += *reinterpret_cast<const f32x4*>(src + ww * kRsTile);
   }
-  auto store_c = [&](const f32x4 (&x)[2]) __attribute__((always_inline)) {
+  auto store_c = [&](const f32x4 (&x)[MT]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
+    for (int v = 0; v < MT; ++v) {
       const int e = 2048 * v + 4 * tid;
       const int row = e / kRsCols, col = col0 + e % kRsCols;
       if (row >= M) continue;
@@ -606,39 +612,41 @@ __global__ void __launch_bounds__(512, 1) resident_split_kernel(StreamArgs p) {
   // resets the counter.  Tagged packets (8 bytes per value, cleared after
   // use) cost 23.2 us here at M = 32: 19 MB of packet traffic per launch.
   const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.partials + (size_t)g * S * kRsTile);
-  bool live[2];
+  bool live[MT];
 #pragma unroll
-  for (int v = 0; v < 2; ++v) {
+  for (int v = 0; v < MT; ++v) {
     live[v] = (2048 * v + 4 * tid) / kRsCols < M;
     if (live[v]) store_coherent(rp, (uint32_t)((r * kRsTile + 2048 * v + 4 * tid) * 4), own[v]);
   }
   if (!splitk_arrive_last(p.counters + g, (uint32_t)S, &s_last, tid)) return;
-  f32x4 t[8][2];
+  f32x4 t[8][MT];
 #pragma unroll
   for (int sp = 0; sp < 8; ++sp)
 #pragma unroll
-    for (int v = 0; v < 2; ++v)
+    for (int v = 0; v < MT; ++v)
       t[sp][v] = sp < S && sp != r && live[v] ? load_coherent4(rp, (uint32_t)((sp * kRsTile + 2048 * v + 4 * tid) * 4))
                                               : own[v];
-  f32x4 tot[2] = {t[0][0], t[0][1]};
+  f32x4 tot[MT];
+#pragma unroll
+  for (int v = 0; v < MT; ++v) tot[v] = t[0][v];
 #pragma unroll
   for (int sp = 1; sp < 8; ++sp)
 #pragma unroll
-    for (int v = 0; v < 2; ++v)
+    for (int v = 0; v < MT; ++v)
       if (sp < S) tot[v] += t[sp][v];
   store_c(tot);
 }
 
 }  // namespace
 
-int64_t resident_splits(int rows, int64_t K) { return rows == 32 ? (K + kRsKr - 1) / kRsKr : 1; }
+int64_t resident_splits(int rows, int64_t K) { return rows >= 16 ? (K + kRsKr - 1) / kRsKr : 1; }
 int64_t resident_groups(int rows, int64_t N) {
-  const int64_t cw = rows == 32 ? kRsCols : 32;
+  const int64_t cw = rows >= 16 ? kRsCols : 32;
   return (N + cw - 1) / cw;
 }
 size_t resident_workspace(int rows, int64_t N, int64_t K) {
   const int64_t S = resident_splits(rows, K);
-  return S > 1 ? (size_t)(resident_groups(rows, N) * S * kRsTile * 4) : 0;
+  return S > 1 ? (size_t)(resident_groups(rows, N) * S * rows * kRsCols * 4) : 0;
 }
 
 // Resident kernel shape rules: [N,K/2], 1 <= M <= rows.  rows 1 or 8: K a
@@ -648,7 +656,7 @@ size_t resident_workspace(int rows, int64_t N, int64_t K) {
 bool resident_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K) {
   if (layout != kLayoutNK || M < 1 || M > rows || N < 1) return false;
   if (rows == 1 || rows == 8) return K >= 512 && K <= 8192 && K % 512 == 0;
-  return rows == 32 && K >= 256 && K % 256 == 0 && resident_splits(rows, K) <= 8 &&
+  return (rows == 16 || rows == 32) && K >= 256 && K % 256 == 0 && resident_splits(rows, K) <= 8 &&
          resident_groups(rows, N) * 4 <= (int64_t)MXFP4_COUNTER_BYTES &&
          resident_workspace(rows, N, K) <= (size_t)kNumRecords;
 }
@@ -656,10 +664,13 @@ bool resident_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K) {
 hipError_t launch_resident(int rows, int layout, const StreamArgs& a, hipStream_t stream) {
   if (!resident_shape_ok(rows, layout, a.M, a.N, a.K) || a.splits != resident_splits(rows, a.K))
     return hipErrorInvalidValue;
-  if (rows == 32) {
+  if (rows >= 16) {
     if (a.splits > 1 && (!a.partials || !a.counters)) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)(resident_groups(rows, a.N) * a.splits);
-    hipLaunchKernelGGL(resident_split_kernel, dim3(grid), dim3(64 * kRsWaves), 0, stream, a);
+    if (rows == 32)
+      hipLaunchKernelGGL(resident_split_kernel<2>, dim3(grid), dim3(64 * kRsWaves), 0, stream, a);
+    else
+      hipLaunchKernelGGL(resident_split_kernel<1>, dim3(grid), dim3(64 * kRsWaves), 0, stream, a);
     return hipGetLastError();
   }
   const dim3 grid((unsigned)((a.N + 31) / 32)), block((unsigned)(a.K / 512 * 64));

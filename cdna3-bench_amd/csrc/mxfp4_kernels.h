@@ -146,8 +146,8 @@ hipError_t launch_decode(int rows, int layout, const StreamArgs& args, hipStream
 // Resident kernels (mxfp4_decode.hip): [N,K/2], every weight load of a CTA
 // issued at entry into VGPRs.  rows = 1 or 8 (M <= rows): one CTA of K / 512
 // waves per 32 columns x the whole K (K % 512 == 0, K <= 8192), no split, no
-// workspace.  rows = 32 (M <= 32): one CTA of 8 waves per 128 columns x 2048
-// K, S = ceil(K / 2048) <= 8 CTAs per column group whose fp32 partials
+// workspace.  rows = 16 or 32 (M <= rows): one CTA of 8 waves per 128
+// columns x 2048 K, S = ceil(K / 2048) <= 8 CTAs per column group whose fp32 partials
 // (resident_workspace bytes after the counters) the last arrival sums.
 int64_t resident_splits(int rows, int64_t K);
 size_t resident_workspace(int rows, int64_t N, int64_t K);

@@ -791,7 +791,9 @@ bool whole_shape(const StreamShape& s) {
 }
 
 bool stream_shape_available(const StreamShape& s) {
-  if (s.resident == 32) return s.mt == 2 && s.waves == 8 && s.gcb == 8 && s.nslot == 0 && s.smax == 8 && s.kw == 256 && s.direct == 0;
+  if (s.resident == 16 || s.resident == 32)
+    return s.mt == s.resident / 16 && s.waves == 8 && s.gcb == 8 && s.nslot == 0 && s.smax == 8 && s.kw == 256 &&
+           s.direct == 0;
   if (s.resident)
     return s.mt == 1 && s.waves == 16 && s.gcb == 2 && s.nslot == 0 && s.smax == 1 && s.kw == 512 &&
            s.direct == 0 && (s.resident == 1 || s.resident == 8);

@@ -59,7 +59,8 @@ enum {
                                (variants 0-4) and whole-K (5, 6: M <= 16) kernels; NK only:
                                decode (7: M <= 16, 8: M <= 8) and resident (9: M == 1,
                                10: M <= 8; K % 512 == 0, K <= 8192; 11: M <= 32,
-                               K % 256 == 0, ceil(K / 2048) <= 8 splits) kernels */
+                               12: M <= 16; K % 256 == 0, ceil(K / 2048) <= 8 splits)
+                               kernels */
 };
 
 /* A launch plan: which kernel family, which tile variant, how many K splits. */

@@ -197,6 +197,9 @@ def test_plan_from_python(kk):
     for N in (8192, 16384, 28672):
         kind, _, split, desc = kk.select_plan(32, N, 8192, "nk")
         assert kind == kk.KERNEL_STREAM and desc.startswith("resident rows32") and split == 4, (N, desc)
+    for N in (16384, 28672):
+        kind, _, split, desc = kk.select_plan(16, N, 8192, "nk")
+        assert kind == kk.KERNEL_STREAM and desc.startswith("resident rows16") and split == 4, (N, desc)
     kind, _, split, desc = kk.select_plan(8, 8192, 8192, "p")
     assert kind == kk.KERNEL_STREAM and desc.startswith("stream-whole") and split == 1
     kind, _, _, desc = kk.select_plan(16, 8192, 8192, "kn")

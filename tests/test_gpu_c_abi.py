@@ -128,22 +128,23 @@ def test_stream_counter_path_matches_poll_path(lib, M, layout):
     assert mo.strict_violations(outs[1][:, cols], ref, K) == 0
 
 
-@pytest.mark.parametrize("M,K", [(32, 8192), (21, 16384 - 256)])
-def test_resident_split_counters_return_to_zero(lib, M, K):
-    """The resident split kernel (variant 11) through mxfp4_gemm_with_plan:
+@pytest.mark.parametrize("variant,M,K", [(11, 32, 8192), (11, 21, 16384 - 256), (12, 16, 8192), (12, 9, 6144)])
+def test_resident_split_counters_return_to_zero(lib, variant, M, K):
+    """The resident split kernel (variants 11, 12) through mxfp4_gemm_with_plan:
     its fp32 partials stay in the workspace, its group counters are zero
     after every call, and repeated calls on the same workspace are bitwise
     identical and within the tolerance of the oracle."""
     import torch
 
     N = 4096
-    log(f"case resident split counters M={M} K={K}")
+    log(f"case resident split counters variant={variant} M={M} K={K}")
     A_bits, W, S = mo.make_inputs(M, N, K, 122, 130, 1.0, seed=M + K)
     A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(W), to_dev_u8(S)
-    plan = Plan(4, 11, -(-K // 2048), 0)
+    plan = Plan(4, variant, -(-K // 2048), 0)
     assert plan.split_k > 1
     wsb = lib.mxfp4_gemm_workspace_bytes(M, N, K, LAYOUT["nk"], ctypes.byref(plan))
-    assert wsb == COUNTER_BYTES + -(-(N // 128) * plan.split_k * 32 * 128 * 4 // 256) * 256
+    rows = 32 if variant == 11 else 16
+    assert wsb == COUNTER_BYTES + -(-(N // 128) * plan.split_k * rows * 128 * 4 // 256) * 256
     ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
     outs = []
     for _ in range(3):

@@ -411,7 +411,8 @@ def test_resident_rejects(kk, variant, rows):
             run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=(kk.KERNEL_STREAM, variant, split))
 
 
-def test_resident_split_variant(kk):
+@pytest.mark.parametrize("variant,rows", [(11, 32), (12, 16)])
+def test_resident_split_variant(kk, variant, rows):
     """Resident split kernel (variant 11: [N,K/2], M <= 32, 128 columns x 2048
     K per CTA, S = ceil(K / 2048) <= 8 splits): one wave's K (K = 256), a
     partial last split, 4 and 8 splits, ragged M and N, fp32 and bf16 out;
@@ -419,13 +420,13 @@ def test_resident_split_variant(kk):
     rounded (the counter-arbitration path: test_gpu_c_abi.py)."""
     import torch
 
-    for M in (1, 17, 32):
+    for M in sorted({1, rows // 2 + 1, rows}):
         for N, K in ((512, 256), (1000, 2048 + 256), (1001, 4096), (4096, 8192), (96, 16384), (200, 6144 + 512)):
             splits = -(-K // 2048)
-            log(f"case resident-split M={M} N={N} K={K} splits={splits}")
+            log(f"case resident-split variant={variant} M={M} N={N} K={K} splits={splits}")
             A_bits, W, S = mo.make_inputs(M, N, K, 118, 134, seed=M + N + K + 17)
             ref = oracle_f64(A_bits, W, S)
-            plan = (kk.KERNEL_STREAM, 11, splits)
+            plan = (kk.KERNEL_STREAM, variant, splits)
             out = run_gemm(kk, A_bits, W, S, "nk", torch.float32, plan=plan)
             bad = mo.strict_violations(out, ref, K)
             assert bad == 0, f"M={M} N={N} K={K}: {bad} bad"
@@ -435,14 +436,15 @@ def test_resident_split_variant(kk):
             assert np.array_equal(out16, mo.bf16_bits_to_f32(mo.f32_to_bf16_bits(out))), f"M={M} N={N} K={K}"
 
 
-def test_resident_split_rejects(kk):
+@pytest.mark.parametrize("variant,rows", [(11, 32), (12, 16)])
+def test_resident_split_rejects(kk, variant, rows):
     import torch
 
-    for M, K, layout, split in ((33, 2048, "nk", 1), (32, 16384 + 256, "nk", 9), (32, 2048 + 128, "nk", 2),
-                                (32, 2048, "p", 1), (32, 2048, "kn", 1), (32, 4096, "nk", 1)):
+    for M, K, layout, split in ((rows + 1, 2048, "nk", 1), (rows, 16384 + 256, "nk", 9), (rows, 2048 + 128, "nk", 2),
+                                (rows, 2048, "p", 1), (rows, 2048, "kn", 1), (rows, 4096, "nk", 1)):
         A_bits, W, S = mo.make_inputs(M, 64, K, 120, 132, seed=4)
         with pytest.raises(RuntimeError, match="invalid argument"):  # M, splits, K % 256, layout, split count
-            run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=(kk.KERNEL_STREAM, 11, split))
+            run_gemm(kk, A_bits, W, S, layout, torch.float32, plan=(kk.KERNEL_STREAM, variant, split))
 
 
 @pytest.mark.parametrize("M", [24, 32])
