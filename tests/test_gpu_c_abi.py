@@ -258,6 +258,47 @@ def test_graph_capture_workspace(lib):
         assert torch.equal(eager, want)
 
 
+@pytest.mark.parametrize("M,N,K,plan_prefix", [(1, 8192, 8192, "resident rows1"), (32, 8192, 8192, "resident rows32"),
+                                                (16, 28672, 8192, "resident rows16")])
+def test_graph_capture_resident(lib, M, N, K, plan_prefix):
+    """The resident kernels (the split forms' fp32 partials and group
+    counters in the stream's workspace) captured in a HIP graph replay the
+    eager result bit for bit, replay after replay, with eager calls of the
+    same plan on the same workspace in between."""
+    import torch
+
+    from mxfp4_cdna3 import kernels as kk
+
+    log(f"case graph capture {plan_prefix} M={M} N={N} K={K}")
+    assert kk.select_plan(M, N, K, "nk")[3].startswith(plan_prefix)
+    A_bits, W, S = mo.make_inputs(M, N, K, 122, 130, 1.0, seed=M + 14)
+    A, B, Sd = to_dev_bf16(A_bits), to_dev_u8(W), to_dev_u8(S)
+    want = kk.gemm(A, B, Sd, None, "nk", torch.bfloat16)
+    torch.cuda.synchronize()
+    C = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        kk.gemm(A, B, Sd, C, "nk")  # allocates this stream's workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        kk.gemm(A, B, Sd, C, "nk")
+    for _ in range(3):
+        C.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(C, want)
+        with torch.cuda.stream(s):
+            eager = kk.gemm(A, B, Sd, None, "nk", torch.bfloat16)  # the same workspace between replays
+        torch.cuda.synchronize()
+        assert torch.equal(eager, want)
+    cols = np.random.default_rng(M).choice(N, 256, replace=False)
+    ref = oracle_f64(A_bits, W, S, np.arange(M), cols)
+    assert mo.strict_violations(want.float().cpu().numpy()[:, cols], ref, K) == 0
+
+
 def test_graph_capture_via_g(lib):
     """A via-G plan ([N,K/2] weights rewritten to G in the stream's workspace,
     then the tiled kernel) captured in a HIP graph replays the eager result,
