@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from oracle import mxfp4_oracle as mo
-from tests.gpu_util import log, oracle_f64, run_gemm, sample_indices, to_dev_bf16, to_dev_u8
+from tests.gpu_util import full_check_fp32, log, oracle_f64, run_gemm, sample_indices, to_dev_bf16, to_dev_u8
 
 pytestmark = pytest.mark.gpu
 
@@ -598,6 +598,12 @@ def _check_config(kk, cfg, layout, rows_k=24, cols_k=1536, strict=True):
     # size-independent property at full size: every output finite, and a row
     # permutation of A permutes C exactly (rows are independent, fixed K order)
     assert np.isfinite(out).all()
+    # every element against a float32 torch reference on the GPU (c = 8: the
+    # 4 of the float64 checks above for our sums plus 4 for the reference's)
+    full_strict, full_canc = full_check_fp32(A_bits, W, S, out, c=8.0)
+    log(f"config {cfg.name} layout={layout}: all {out.size} elements against the float32 reference: strict "
+        f"violations {full_strict}, cancellation-aware (c=8) violations {full_canc}")
+    assert full_canc == 0
     return A_bits, W, S, out
 
 
