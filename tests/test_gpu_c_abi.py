@@ -220,6 +220,8 @@ def test_split_k_on_two_streams(lib):
         assert torch.equal(o, want)
 
 
+# the refused capture ends with an empty graph, which torch reports
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
 def test_graph_capture_workspace(lib):
     import torch
 
