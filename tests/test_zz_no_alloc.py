@@ -58,10 +58,13 @@ def test_noalloc_matches_mxfp4_gemm(lib):
     import torch
 
     # a split-K tiled plan (about 29 MiB of partials), a via-G plan (the
-    # [N,K/2] weights rewritten to G in the scratch, after the counters),
-    # then a smaller streaming split-K plan: each call reuses what the one
-    # before left, and the last finds its counters zero
-    cases = [(128, 28672, 8192, "kn", 1, 31), (2048, 4096, 4096, "nk", 1, 33), (16, 8192, 8192, "nk", 0, 32)]
+    # [N,K/2] weights rewritten to G in the scratch, after the counters), the
+    # resident split kernel (fp32 partials left in the scratch), then a
+    # smaller streaming split-K plan whose packet region holds those untagged
+    # partials: each call reuses what the one before left, and the last finds
+    # its counters zero
+    cases = [(128, 28672, 8192, "kn", 1, 31), (2048, 4096, 4096, "nk", 1, 33), (32, 8192, 8192, "nk", 0, 34),
+             (16, 8192, 8192, "nk", 0, 32)]
     for M, N, K, layout, c_dtype, seed in cases:
         log(f"case mxfp4_gemm_noalloc M={M} N={N} K={K} layout={layout} c_dtype={c_dtype}")
         wsb = lib.mxfp4_gemm_workspace_bytes(M, N, K, LAYOUT[layout], None)
