@@ -46,11 +46,11 @@ struct TiledVariant {
 // Variants 6, 7 and 15: the median over the MFMA-bound BASELINE configs
 // (dit_up, dit_down, 70B FFN M = 512 / 2048 / 8192) of peak time / measured
 // time, fitted from a bench.py --sweep CSV by cost_model.fit_efficiency
-// (eff_kn is the [K/2,N] fit; G measures 0.585 / 0.504 / 0.441); 3 and 5
+// (eff_kn is the [K/2,N] fit; G measures 0.580 / 0.497 / 0.437); 3 and 5
 // were measured after the split-K reduction change at M = 48 .. 1024 and
-// scaled by the sweep box's clock (x 1.022, variant 15's refit) so their
-// standing against the fitted variants is kept.  The model then picks within
-// 12 % of the best measured plan on those shapes.
+// are scaled with variant 15 at each refit, per layout, so their standing
+// against the fitted variants is kept.  The model then picks within 12 % of
+// the best measured plan on those shapes.
 const TiledVariant kTiled[] = {
     // 0, 1, 2, 4, 8 .. 14: explicit plans only (efficiency 0: never
     // auto-selected); their last calibration predates the store-loop and
@@ -58,11 +58,11 @@ const TiledVariant kTiled[] = {
     {{2, 2, 4}, 0.0, 0.0, 1, kFamilyPlain},         // 0: 256 x 256, 4 waves, 128 x 128 per wave
     {{4, 2, 2}, 0.0, 0.0, 1, kFamilyPlain},         // 1: 256 x 256, 8 waves
     {{2, 2, 2}, 0.0, 0.0, 2, kFamilyPlain},         // 2: 128 x 256
-    {{1, 2, 2}, 0.174, 0.153, 2, kFamilyPlain},     // 3:  64 x 256 (re-measured at M = 64 .. 256)
+    {{1, 2, 2}, 0.173, 0.150, 2, kFamilyPlain},     // 3:  64 x 256 (re-measured at M = 64 .. 256)
     {{2, 1, 2}, 0.0, 0.0, 2, kFamilyPlain},         // 4: 128 x 128
-    {{1, 2, 1}, 0.153, 0.133, 4, kFamilyPlain},     // 5:  32 x 256 (re-measured at M = 48 .. 1024)
-    {{4, 2, 2, 4, 3}, 0.505, 0.482, 1, kFamilyPipe}, // 6: pipelined 256 x 256, 8 waves of 64 x 128, 3 stages
-    {{2, 2, 2, 4, 3}, 0.443, 0.402, 1, kFamilyPipe}, // 7: pipelined 128 x 256, 4 waves of 64 x 128
+    {{1, 2, 1}, 0.152, 0.131, 4, kFamilyPlain},     // 5:  32 x 256 (re-measured at M = 48 .. 1024)
+    {{4, 2, 2, 4, 3}, 0.501, 0.475, 1, kFamilyPipe}, // 6: pipelined 256 x 256, 8 waves of 64 x 128, 3 stages
+    {{2, 2, 2, 4, 3}, 0.431, 0.390, 1, kFamilyPipe}, // 7: pipelined 128 x 256, 4 waves of 64 x 128
     {{4, 2, 2, 4, 3}, 0.0, 0.0, 1, kFamilyPipe},   // 8: = 6 (a 4-stage 256 x 256 ring no longer fits 160 KB)
     {{2, 4, 4, 2, 3}, 0.0, 0.0, 1, kFamilyPipe},   // 9: = 10
     {{2, 4, 4, 2, 3}, 0.0, 0.0, 1, kFamilyPipe},   // 10: pipelined 256 x 256, 8 waves of 128 x 64, 3 stages
@@ -70,7 +70,7 @@ const TiledVariant kTiled[] = {
     {{2, 4, 2, 2, 4}, 0.0, 0.0, 1, kFamilyPipe},   // 12: pipelined 128 x 256, 8 waves of 64 x 64
     {{1, 4, 4, 2, 4}, 0.0, 0.0, 1, kFamilyPipe},   // 13: pipelined 128 x 256, 4 waves of 128 x 64
     {{2, 1, 2, 4, 4}, 0.0, 0.0, 2, kFamilyPipe},   // 14: pipelined 128 x 128, 2 waves
-    {{2, 2, 2, 4, 3}, 0.565, 0.500, 2, kFamilySched}, // 15: hand-scheduled 128 x 256, 4 waves of 64 x 128, 2 CTAs / CU
+    {{2, 2, 2, 4, 3}, 0.561, 0.491, 2, kFamilySched}, // 15: hand-scheduled 128 x 256, 4 waves of 64 x 128, 2 CTAs / CU
 };
 constexpr int kNumTiled = sizeof(kTiled) / sizeof(kTiled[0]);
 
