@@ -101,6 +101,7 @@ const StreamShape kStream[] = {
     {1, 16, 2, 0, 1, 512, 0, 8},  // 10: resident kernel, M <= 8 (explicit plans only)
     {2, 8, 8, 0, 8, 256, 0, 32},  // 11: resident split kernel, M <= 32, [N,K/2], 128 columns x 2048 K per CTA, K % 256 == 0
     {1, 8, 8, 0, 8, 256, 0, 16},  // 12: resident split kernel, M <= 16, two CTAs per CU
+    {1, 16, 2, 1, 1, 512, 0, 1},  // 13: resident kernel, M == 1, whole-segment loads and dot products
 };
 constexpr int kNumStream = sizeof(kStream) / sizeof(kStream[0]);
 constexpr int kStreamSpin = 4096;  // late-unit polls before counter arbitration
@@ -197,10 +198,11 @@ void choose_gemv(int layout, int64_t M, int64_t N, int64_t K, mxfp4_plan* out) {
     // 2 <= M <= 8 with [N,K/2]: the decode kernel with the activations in LDS
     // (variant 8) before those (M = 8: 11.8 / 39.4 us against 12.3 / 41.0 us
     // whole-K; at M = 1 the whole-K kernel is faster, 10.4 against 11.1 us).
-    // M == 1 with [N,K/2] and K % 512 == 0, K <= 8192: the resident kernel
-    // (variant 9) before those (N = 8192 / 28672, K = 8192: 10.0 / 26.9 us
-    // against 10.4 / 33.6 us whole-K).
-    static const int kPrefer1[] = {9, 6, 5, 3, 0, 1}, kPrefer8[] = {8, 6, 5, 3, 0, 1}, kPrefer16[] = {3, 0, 1},
+    // M == 1 with [N,K/2] and K % 512 == 0, K <= 8192: the resident kernel's
+    // dot-product form (variant 13) before those (N = 8192 / 28672, K = 8192:
+    // 9.4 / 25.9 us against 10.0 / 27.1 us for its MFMA form, variant 9, and
+    // 10.4 / 33.6 us whole-K).
+    static const int kPrefer1[] = {13, 6, 5, 3, 0, 1}, kPrefer8[] = {8, 6, 5, 3, 0, 1}, kPrefer16[] = {3, 0, 1},
                      kPrefer32[] = {4, 2};
     const int* pref = two ? kPrefer32 : M == 1 ? kPrefer1 : M <= 8 ? kPrefer8 : kPrefer16;
     const int npref = two ? 2 : M == 1 ? 6 : M <= 8 ? 6 : 3;
@@ -651,7 +653,8 @@ hipError_t mxfp4_plan_describe(const mxfp4_plan* plan, char* buf, size_t buf_len
         snprintf(buf, buf_len, "resident rows%d cols%d kr%d split%d", s.resident, 16 * s.gcb, s.k_split(),
                  plan->split_k);
       else if (s.resident)
-        snprintf(buf, buf_len, "resident rows%d cols%d split%d", s.resident, 16 * s.gcb, plan->split_k);
+        snprintf(buf, buf_len, "resident rows%d cols%d split%d%s", s.resident, 16 * s.gcb, plan->split_k,
+                 s.nslot == 1 ? " dot" : "");
       else if (s.direct)
         snprintf(buf, buf_len, "decode rows%d cols%d kr%d split%d", s.direct, 16 * s.gcb, s.k_split(),
                  plan->split_k);

@@ -452,6 +452,85 @@ __global__ void __launch_bounds__(1024, 1) resident_kernel(StreamArgs p) {
 }
 
 // ---- resident split kernel: 17 <= M <= 32 ------------------------------------
+// M = 1 form with whole column segments per load (variant 13).  A bare read
+// of the decode weights with 4 columns x 256 contiguous bytes per load takes
+// 7.1 us against 7.9 us in the MFMA operand order (16 columns x 64 bytes).
+// At M = 1 an MFMA uses one row of 16, so this form drops it: lane (r, e) of
+// load j holds bytes 16e .. 16e+15 (K 32e .. 32e+31 of the wave's 512) of
+// column 4j + r, converts them with their scale and takes v_dot2_f32_bf16
+// products with the same 32 activations in K order; the 16 lanes of a
+// column are summed by xor shuffles (8, 4, 2, 1) and the waves in wave order.
+// A word as the bf16 pair operand of v_dot2_f32_bf16.  Taken by value: a
+// __builtin_bit_cast of a vector component (v.y) read component 0 here.
+__device__ __forceinline__ bf16x2 bf16_pair(uint32_t v) { return __builtin_bit_cast(bf16x2, v); }
+
+// OCC = 8 waves per SIMD (<= 64 VGPRs: two 16-wave CTAs share a CU) for grids
+// past one CTA per CU; OCC = 1 otherwise (66 VGPRs; measured at M = 1, K =
+// 8192: 9.4 against 9.9 us at N = 8192, and 28.7 against 25.9 us at N =
+// 28672, where it fits one CTA per CU).
+template <int OCC>
+__global__ void __launch_bounds__(1024, OCC) resident_dot_kernel(StreamArgs p) {
+  __shared__ __attribute__((aligned(16))) float red[16][32];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = (int)(blockDim.x >> 6);
+  const int r = lane >> 4, e = lane & 15;
+  const int N = p.N, K = p.K;
+  const int col0 = 32 * (int)blockIdx.x;
+  const size_t Kh = (size_t)(K >> 1), G = (size_t)(K >> 5);
+
+  u32x4 av[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) av[s] = *reinterpret_cast<const u32x4*>(p.A + 512 * w + 32 * e + 8 * s);
+  uint32_t sb[8];
+  u32x4 wv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sb[j] = p.S[(size_t)min(col0 + 4 * j + r, N - 1) * G + 16 * w + e];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    wv[j] = *reinterpret_cast<const u32x4*>(p.B + (size_t)min(col0 + 4 * j + r, N - 1) * Kh + 256 * w + 16 * e);
+
+  for (int i = (int)threadIdx.x; i < (16 - nw) * 32; i += (int)blockDim.x) red[nw + i / 32][i % 32] = 0.f;
+
+  float part[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float f = e8m0_to_f32(sb[j]);
+    float acc = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t b0 = fp4x2_to_bf16x2<0>(wv[j][d], f), b1 = fp4x2_to_bf16x2<1>(wv[j][d], f);
+      const uint32_t b2 = fp4x2_to_bf16x2<2>(wv[j][d], f), b3 = fp4x2_to_bf16x2<3>(wv[j][d], f);
+      acc = __builtin_amdgcn_fdot2_f32_bf16(bf16_pair(b0), bf16_pair(av[d].x), acc, false);
+      acc = __builtin_amdgcn_fdot2_f32_bf16(bf16_pair(b1), bf16_pair(av[d].y), acc, false);
+      acc = __builtin_amdgcn_fdot2_f32_bf16(bf16_pair(b2), bf16_pair(av[d].z), acc, false);
+      acc = __builtin_amdgcn_fdot2_f32_bf16(bf16_pair(b3), bf16_pair(av[d].w), acc, false);
+    }
+    part[j] = acc;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) part[j] += __shfl_xor(part[j], m, 16);
+  if (e == 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) red[w][4 * j + r] = part[j];
+  }
+  __syncthreads();
+  if (threadIdx.x < 32) {
+    const int col = col0 + (int)threadIdx.x;
+    if (col >= N) return;
+    float x = red[0][threadIdx.x];
+#pragma unroll
+    for (int ww = 1; ww < 16; ++ww) x += red[ww][threadIdx.x];
+    const float y = p.ep.any ? epilogue_value(p.ep, x, 0, col, N) : x;
+    if (p.out_bf16)
+      static_cast<uint16_t*>(p.C)[col] = (uint16_t)bf16_bits_rne(y);
+    else
+      static_cast<float*>(p.C)[col] = y;
+  }
+}
+
 // One CTA of 8 waves per 128 columns x 2048 K (S = ceil(K / 2048) CTAs per
 // column group); wave w owns K 256w .. 256w+255 of the CTA's range.  At entry
 // every wave issues its 32 activation rows (16 loads of 1 KB: 2 rows x 512 B
@@ -659,6 +738,16 @@ bool resident_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K) {
   return (rows == 16 || rows == 32) && K >= 256 && K % 256 == 0 && resident_splits(rows, K) <= 8 &&
          resident_groups(rows, N) * 4 <= (int64_t)MXFP4_COUNTER_BYTES &&
          resident_workspace(rows, N, K) <= (size_t)kNumRecords;
+}
+
+hipError_t launch_resident_dot(int layout, const StreamArgs& a, hipStream_t stream) {
+  if (!resident_shape_ok(1, layout, a.M, a.N, a.K) || a.splits != 1) return hipErrorInvalidValue;
+  const unsigned grid = (unsigned)((a.N + 31) / 32), block = (unsigned)(a.K / 512 * 64);
+  if (grid > 256)
+    hipLaunchKernelGGL(resident_dot_kernel<8>, dim3(grid), dim3(block), 0, stream, a);
+  else
+    hipLaunchKernelGGL(resident_dot_kernel<1>, dim3(grid), dim3(block), 0, stream, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_resident(int rows, int layout, const StreamArgs& a, hipStream_t stream) {

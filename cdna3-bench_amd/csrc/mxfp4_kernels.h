@@ -153,6 +153,9 @@ int64_t resident_splits(int rows, int64_t K);
 size_t resident_workspace(int rows, int64_t N, int64_t K);
 bool resident_shape_ok(int rows, int layout, int64_t M, int64_t N, int64_t K);
 hipError_t launch_resident(int rows, int layout, const StreamArgs& args, hipStream_t stream);
+// M = 1 form with whole 256-byte column segments per load and dot products
+// instead of MFMAs (StreamShape::nslot = 1); shape rules of rows = 1.
+hipError_t launch_resident_dot(int layout, const StreamArgs& args, hipStream_t stream);
 
 // Any shape with K % 32 == 0; one thread per output, for shapes the fast
 // families do not cover (N % 16 != 0, unaligned pointers).

@@ -795,8 +795,8 @@ bool stream_shape_available(const StreamShape& s) {
     return s.mt == s.resident / 16 && s.waves == 8 && s.gcb == 8 && s.nslot == 0 && s.smax == 8 && s.kw == 256 &&
            s.direct == 0;
   if (s.resident)
-    return s.mt == 1 && s.waves == 16 && s.gcb == 2 && s.nslot == 0 && s.smax == 1 && s.kw == 512 &&
-           s.direct == 0 && (s.resident == 1 || s.resident == 8);
+    return s.mt == 1 && s.waves == 16 && s.gcb == 2 && (s.nslot == 0 || (s.nslot == 1 && s.resident == 1)) &&
+           s.smax == 1 && s.kw == 512 && s.direct == 0 && (s.resident == 1 || s.resident == 8);
   if (s.direct)
     return s.mt == 1 && s.waves == 8 && s.nslot == 0 && s.smax == 8 &&
            ((s.direct == 16 && s.gcb == 4 && s.kw == 512) || (s.direct == 8 && s.gcb == 2 && s.kw == 1024));
@@ -810,7 +810,8 @@ bool stream_shape_available(const StreamShape& s) {
 }
 
 hipError_t launch_stream(int layout, const StreamShape& s, const StreamArgs& args, hipStream_t stream) {
-  if (s.resident) return launch_resident(s.resident, layout, args, stream);
+  if (s.resident)
+    return s.nslot == 1 ? launch_resident_dot(layout, args, stream) : launch_resident(s.resident, layout, args, stream);
   if (s.direct) return launch_decode(s.direct, layout, args, stream);
   if (whole_shape(s)) {
     if (args.splits != 1) return hipErrorInvalidValue;

@@ -57,8 +57,8 @@ enum {
   MXFP4_KERNEL_GENERIC = 3, /* one thread per output, any N */
   MXFP4_KERNEL_STREAM = 4   /* weight streaming, M <= 32, NK or P layout, K % 256 == 0: split-K
                                (variants 0-4) and whole-K (5, 6: M <= 16) kernels; NK only:
-                               decode (7: M <= 16, 8: M <= 8) and resident (9: M == 1,
-                               10: M <= 8; K % 512 == 0, K <= 8192; 11: M <= 32,
+                               decode (7: M <= 16, 8: M <= 8) and resident (9 and 13:
+                               M == 1, 10: M <= 8; K % 512 == 0, K <= 8192; 11: M <= 32,
                                12: M <= 16; K % 256 == 0, ceil(K / 2048) <= 8 splits)
                                kernels */
 };

@@ -93,9 +93,10 @@ def test_epilogue_gemv(kk, layout, plan):
 @pytest.mark.parametrize("layout,plan", [("nk", (4, 3, 2)), ("p", (4, 0, 4)), ("nk", (4, 2, 1)),
                                          ("nk", (4, 5, 1)), ("p", (4, 6, 1)), ("nk", (4, 7, 2)), ("nk", (4, 8, 1)),
                                          ("nk", (4, 8, 2)), ("nk", (4, 9, 1)), ("nk", (4, 10, 1)),
-                                         ("nk", (4, 11, 1)), ("nk", (4, 11, 4)), ("nk", (4, 12, 4))])
+                                         ("nk", (4, 11, 1)), ("nk", (4, 11, 4)), ("nk", (4, 12, 4)),
+                                         ("nk", (4, 13, 1))])
 def test_epilogue_stream(kk, layout, plan):
-    M = 32 if plan[1] in (2, 11) else 8 if plan[1] in (8, 10) else 1 if plan[1] == 9 else 16
+    M = 32 if plan[1] in (2, 11) else 8 if plan[1] in (8, 10) else 1 if plan[1] in (9, 13) else 16
     K = 16384 if plan[1] == 8 and plan[2] > 1 else 8192 if plan[2] > 1 else 1024
     check(kk, M, 1024, K, layout, plan, seed=2)
 

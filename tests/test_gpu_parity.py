@@ -374,7 +374,7 @@ def test_decode_rejects(kk, variant, rows, kr, kg):
 
 
 # resident kernel variants: (variant, rows)
-RESIDENT_VARIANTS = [(9, 1), (10, 8)]
+RESIDENT_VARIANTS = [(9, 1), (10, 8), (13, 1)]  # 13: the M = 1 form with dot products
 
 
 @pytest.mark.parametrize("variant,rows", RESIDENT_VARIANTS)
